@@ -1,0 +1,204 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X DVAttn operators on the five BASELINE configurations.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--no-cpu]
+
+One "step" is one call of the operator over one batch of synthetic, seeded
+inputs already resident in HBM.  The headline line (``value``) is configuration
+2 (bf16 paged GQA-16 decode, batch 32, KV length U[1024, 8192], page 16): K
+steps are timed back to back between two synchronisations; ``value`` is the
+achieved algorithmic HBM rate in TB/s and ``ms_per_step`` the time per call.
+Inputs rotate over enough replicas that consecutive calls never find their K/V
+in the 256 MB Infinity Cache (cold HBM reads, as in a real multi-layer decode
+step).  Every configuration is also reported under ``per_config``.
+
+``roofline`` covers the decode kernel family (decode + split-merge launch of one
+call), timed with HIP events on the stream the kernels run on.  ``cpu_baseline``
+times the CPU oracle (the fp32 restatement of the reference's eager path) on a
+bounded sample of configuration 2, on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E
+MFMA_BF16_PEAK_TFLOPS = 2500.0   # dense bf16/fp16
+METRIC = "paged decode-attn µs/call + achieved HBM TB/s (% of peak), bf16 GQA-16"
+MALL_BYTES = 256 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def replicas_for(wl_bytes: int, max_replicas: int = 8) -> int:
+    # enough distinct inputs that the rotation's footprint is >= 4x the Infinity Cache
+    need = max(1, -(-4 * MALL_BYTES // max(1, wl_bytes)))
+    return min(max_replicas, need)
+
+
+def time_config(i: int, steps: int, warmup: int, device) -> dict:
+    from dvattention_amd import workloads as WL
+    first = WL.config(i, device=device, seed=1234)
+    R = replicas_for(first.meta.get("kv_bytes", first.alg_bytes))
+    wls = [first] + [WL.config(i, device=device, seed=1234 + r) for r in range(1, R)]
+    outs = [w.out_like() for w in wls]
+    rqs = [torch.empty(w.meta["rq_shape"], dtype=w.dtype, device=device) if w.op == "fused" else None for w in wls]
+    for j in range(warmup):
+        WL.run(wls[j % R], outs[j % R], rqs[j % R])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    # (a) K back-to-back steps between two synchronisations (wall clock + events)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ev0.record(stream)
+    for j in range(steps):
+        WL.run(wls[j % R], outs[j % R], rqs[j % R])
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    ms_step = ev0.elapsed_time(ev1) / steps
+    # (b) per-call kernel time: events around each call on the launch stream
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    for j in range(steps):
+        a, b = evs[j]
+        a.record(stream)
+        WL.run(wls[j % R], outs[j % R], rqs[j % R])
+        b.record(stream)
+    torch.cuda.synchronize()
+    per_call = sorted(a.elapsed_time(b) for a, b in evs)
+    kern_ms = sum(per_call) / len(per_call)
+    med_ms = per_call[len(per_call) // 2]
+    alg = sum(w.alg_bytes for w in wls) / R
+    flops = sum(w.flops for w in wls) / R
+    res = {
+        "config": i,
+        "workload": first.name,
+        "op": first.op,
+        "dtype": str(first.dtype).replace("torch.", ""),
+        "replicas": R,
+        "us_per_call": round(ms_step * 1e3, 2),
+        "us_per_call_wall": round(wall * 1e6, 2),
+        "kernel_us_mean": round(kern_ms * 1e3, 2),
+        "kernel_us_median": round(med_ms * 1e3, 2),
+        "alg_bytes": int(alg),
+        "alg_flops": int(flops),
+        "achieved_GBs": round(alg / (kern_ms * 1e-3) / 1e9, 1),
+        "hbm_frac": round(alg / (kern_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "achieved_TFLOPs": round(flops / (kern_ms * 1e-3) / 1e12, 2),
+        "mfma_frac": round(flops / (kern_ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+    }
+    del wls, outs, rqs
+    torch.cuda.empty_cache()
+    return res
+
+
+def cpu_baseline(device, budget_s: float = 20.0) -> dict:
+    """Oracle (fp32 torch-CPU restatement of the reference's eager path) on a
+    bounded sample of configuration 2: the first n sequences, all heads."""
+    from dvattention_amd import workloads as WL
+    from oracle import dvattn_oracle as O
+    cores = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(cores)
+    wl = WL.config(2, device="cpu", seed=1234)
+    t = wl.t
+    Hkv, E = wl.meta["Hkv"], 128
+    lengths = wl.meta["lengths"]
+    done_bytes, done_s, n = 0, 0.0, 0
+    while n < len(lengths) and done_s < budget_s:
+        w = n
+        sl = slice(w, w + 1)
+        t0 = time.perf_counter()
+        O.paged_sdpa(wl.scale, t["locations"][:, sl], t["queries"][sl], t["cosines"][:, sl], t["sines"][:, sl],
+                     t["fragment_lengths"], t["k_cache"], t["v_cache"], t["block_tables"][sl])
+        done_s += time.perf_counter() - t0
+        done_bytes += lengths[w] * Hkv * 2 * E * 2 + 2 * 16 * Hkv * E * 2
+        n += 1
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {
+        "value": round(done_bytes / done_s / 1e12, 6),
+        "unit": "TB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"config 2, first {n} of 32 sequences (all 128 heads), {done_s:.1f} s, "
+                  f"fp32 torch-CPU oracle, {cpu_model or platform.processor()}, torch {torch.__version__}",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (the operator has no multi-GPU path); "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 2
+    import dvattention_amd  # noqa: F401  (loads the HIP libraries; fails loudly if missing)
+    device = torch.device("cuda", 0)
+    cfgs = [int(x) for x in args.configs.split(",") if x]
+    if 2 not in cfgs:
+        cfgs = [2] + cfgs
+    per = {}
+    for i in cfgs:
+        r = time_config(i, args.steps, args.warmup, device)
+        per[i] = r
+        log(f"[bench] cfg{i} {r['workload']}: {r['us_per_call']} us/call (events, back-to-back), "
+            f"kernel {r['kernel_us_mean']} us, {r['achieved_GBs']} GB/s = {100 * r['hbm_frac']:.1f}% HBM, "
+            f"{r['achieved_TFLOPs']} TFLOP/s")
+    head = per[2]
+    cpu = None if args.no_cpu else cpu_baseline(device)
+    line = {
+        "metric": METRIC,
+        "value": round(head["alg_bytes"] / (head["us_per_call"] * 1e-6) / 1e12, 4),
+        "unit": "TB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(head["us_per_call"] / 1e3, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v, random page permutation)",
+        "config": {"workload": head["workload"], "op": "dvattn_paged_sdpa", "batch": 32, "kv_heads": 8,
+                   "q_heads": 128, "head_dim": 128, "page_size": 16, "kv_len": "U[1024,8192]",
+                   "rotary_dim": 128, "replicas": head["replicas"]},
+        "roofline": {"bound": "hbm", "achieved": head["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": head["hbm_frac"], "traffic": None,
+                     "kernel": "dv_decode + dv_merge (one call)", "alg_bytes_per_launch": head["alg_bytes"],
+                     "launch_us": head["kernel_us_mean"]},
+        "cpu_baseline": cpu,
+        "per_config": [per[i] for i in sorted(per)],
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

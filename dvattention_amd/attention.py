@@ -1,0 +1,137 @@
+"""Python operator API, mirroring python/dvattn/attention.py:17-88 of the reference.
+
+Every ``dvattn_*`` wrapper calls ``torch.ops.libdvatt.<op>`` (registered by
+``_libdvatt.so`` over the HIP kernels); there is no eager fallback.  The
+function names, argument order and defaults are the reference's; the paged /
+varlen operators, which the reference exposes only through ``torch.ops``, get
+thin wrappers as well.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+
+def dvattn_fused(queries: torch.Tensor, locations: torch.Tensor, keys: list, values: list,
+                 scale: float, fragment_lengths, cosines: torch.Tensor, sines: torch.Tensor, *,
+                 rotated_queries, out):
+    """Rope + attention over contiguous views (attention.py:17-21).
+
+    queries ``[W,Hq,S,E]``, cosines/sines ``[F,W,S,R]`` fp32; writes the rotated
+    queries ``[F,W,Hq,S,E]`` into ``rotated_queries`` and the result into ``out``.
+    """
+    torch.ops.libdvatt.dvattn_fused(out, rotated_queries, scale, locations, queries.contiguous(),
+                                    fragment_lengths, keys, values, cosines, sines)
+    return out
+
+
+def dvattn_sdpa(queries: torch.Tensor, locations: torch.Tensor, keys: list, values: list,
+                scale: float, fragment_lengths=None, out=None) -> torch.Tensor:
+    """Attention of already-rotated queries ``[F,W,Hq,S,E]`` over contiguous views
+    (attention.py:24-33)."""
+    if out is None:
+        out = torch.empty((queries.size(1), queries.size(2), queries.size(3), values[0].size(-1)),
+                          dtype=queries.dtype, device=queries.device)
+    if fragment_lengths is None:
+        fragment_lengths = torch.tensor([k.size(-2) for k in keys], dtype=torch.int32, device=queries.device)
+    keys = [k.contiguous() for k in keys]
+    values = [v.contiguous() for v in values]
+    torch.ops.libdvatt.dvattn_sdpa(out, scale, locations, queries.contiguous(), fragment_lengths, keys, values)
+    return out
+
+
+def dvattn_rope(queries: torch.Tensor, cosines: torch.Tensor, sines: torch.Tensor, out=None):
+    """Rotate ``[W,Hq,S,E]`` queries once per view -> ``[F,W,Hq,S,E]`` (attention.py:68-72)."""
+    if out is None:
+        out = torch.empty((cosines.size(0), queries.size(0), queries.size(1), queries.size(2), queries.size(3)),
+                          dtype=queries.dtype, device=queries.device)
+    torch.ops.libdvatt.dvattn_rope(out, queries, cosines, sines)
+    return out
+
+
+def dvattn_varlen_rope(queries: torch.Tensor, cosines: torch.Tensor, sines: torch.Tensor, out=None):
+    """Rotate packed ``[T,H,E]`` queries with half-width cos/sin ``[F,T,R/2]`` -> ``[F,T,H,E]``
+    (op ``dvattn_varlen_rope``, binding.cu:205-247)."""
+    if out is None:
+        out = torch.empty((cosines.size(0),) + tuple(queries.shape), dtype=queries.dtype, device=queries.device)
+    torch.ops.libdvatt.dvattn_varlen_rope(out, queries, cosines, sines)
+    return out
+
+
+def dvattn_paged_sdpa(queries: torch.Tensor, locations: torch.Tensor, cosines: torch.Tensor, sines: torch.Tensor,
+                      fragment_lengths: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                      block_tables: torch.Tensor, scale: float, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Paged multi-view decode attention with fused query rotation (op
+    ``dvattn_paged_sdpa``, binding.cu:151-203).  queries ``[W,Hq,S,E]`` ->
+    out ``[W,Hq,S,Ev]``."""
+    if out is None:
+        out = torch.empty(tuple(queries.shape[:3]) + (v_cache.size(-1),), dtype=queries.dtype,
+                          device=queries.device)
+    torch.ops.libdvatt.dvattn_paged_sdpa(out, scale, locations, queries, cosines, sines, fragment_lengths,
+                                         k_cache, v_cache, block_tables)
+    return out
+
+
+def dvattn_varlen_paged_sdpa(queries: torch.Tensor, locations: torch.Tensor, cosines: torch.Tensor,
+                             sines: torch.Tensor, fragment_lengths: torch.Tensor, k_cache: torch.Tensor,
+                             v_cache: torch.Tensor, block_tables: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                             cu_seqlens_k: torch.Tensor, scale: float,
+                             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Varlen (packed tokens) paged multi-view attention (op
+    ``dvattn_varlen_paged_sdpa``, binding.cu:249-296).  queries ``[T,Hq,E]`` ->
+    out ``[T,Hq,Ev]``."""
+    if out is None:
+        out = torch.empty(tuple(queries.shape[:2]) + (v_cache.size(-1),), dtype=queries.dtype,
+                          device=queries.device)
+    torch.ops.libdvatt.dvattn_varlen_paged_sdpa(out, scale, locations, queries, cosines, sines, fragment_lengths,
+                                                k_cache, v_cache, block_tables, cu_seqlens_q, cu_seqlens_k)
+    return out
+
+
+def dvattn_sdpa_pt(queries: torch.Tensor, locations: torch.Tensor, keys: list, values: list,
+                   scale: float, return_intermediate_results: bool = False):
+    """The reference's pure-PyTorch debugging helper (attention.py:36-65), kept
+    for API compatibility.  It is not used by any operator of this package."""
+    qk = []
+    vals = []
+    for f in range(len(keys)):
+        key = keys[f].repeat_interleave(queries.size(-3) // keys[f].size(-3), -3)
+        val = values[f].repeat_interleave(queries.size(-3) // values[f].size(-3), -3)
+        kp = torch.arange(0, key.size(-2), dtype=torch.int32, device=key.device)[None, None, None, :]
+        qp = locations[f][:, None, :, None]
+        mask = kp > qp
+        att = queries[f].to(torch.float32) @ key.transpose(-1, -2).to(torch.float32)
+        att.masked_fill_(mask, float("-inf"))
+        qk.append(att)
+        vals.append(val)
+    qk = torch.concat(qk, dim=-1)
+    vals = torch.concat(vals, dim=-2).to(torch.float32)
+    att = torch.softmax(scale * qk, dim=-1)
+    result = att @ vals
+    if return_intermediate_results:
+        return result, qk, att
+    return result.to(queries.dtype)
+
+
+def rotate_half(x):
+    """Rotates half the hidden dims of the input (attention.py:75-79)."""
+    x1 = x[..., : x.shape[-1] // 2]
+    x2 = x[..., x.shape[-1] // 2:]
+    return torch.cat((-x2, x1), dim=-1)
+
+
+def apply_rotary_pos_emb(x, cos, sin, unsqueeze_dim=1):
+    """Partial RoPE on the first ``cos.shape[-1]`` dims (attention.py:82-88)."""
+    cos = cos.unsqueeze(unsqueeze_dim)
+    sin = sin.unsqueeze(unsqueeze_dim)
+    rotary_dim = cos.shape[-1]
+    x_rot, x_pass = x[..., :rotary_dim], x[..., rotary_dim:]
+    x_rot_emb = (x_rot * cos) + (rotate_half(x_rot) * sin)
+    return torch.cat((x_rot_emb, x_pass), dim=-1).to(x.dtype)
+
+
+__all__ = [
+    "dvattn_fused", "dvattn_sdpa", "dvattn_rope", "dvattn_varlen_rope", "dvattn_paged_sdpa",
+    "dvattn_varlen_paged_sdpa", "dvattn_sdpa_pt", "rotate_half", "apply_rotary_pos_emb",
+]

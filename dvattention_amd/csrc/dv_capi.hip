@@ -1,0 +1,360 @@
+// C ABI of libdvattn_amd.so (declared in include/dvattn_amd.h).  Validates the
+// arguments the reference's torch binding validated (src/binding.cu:41-296),
+// rejects the shapes/dtypes it silently ignored, and launches the gfx950
+// kernels on the caller's stream.  No exception crosses this boundary.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <vector>
+
+#include "../../include/dvattn_amd.h"
+#include "dv_common.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+dvattn_status fail(dvattn_status st, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return st;
+}
+
+dvattn_status ok() {
+    g_err[0] = '\0';
+    return DVATTN_OK;
+}
+
+dvattn_status hip_fail(hipError_t e, const char* what) {
+    return fail(DVATTN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool valid_dtype(int dt) { return dt == DVATTN_F32 || dt == DVATTN_F16 || dt == DVATTN_BF16; }
+
+int log2_exact(int v) {
+    if (v <= 0 || (v & (v - 1))) return -1;
+    int s = 0;
+    while ((1 << s) < v) ++s;
+    return s;
+}
+
+int current_device(int device) {
+    if (device >= 0) return device;
+    int d = 0;
+    if (hipGetDevice(&d) != hipSuccess) d = 0;
+    return d;
+}
+
+// Checks shared by the attention entry points: GQA 16, E == Ev == 128
+// (paged_kernel_v21.cuh:413, varlen:410, kernel_v21.cuh:400).
+dvattn_status check_heads(const dvattn_shape* s) {
+    if (s->Hkv <= 0) return fail(DVATTN_ERR_INVALID, "Hkv must be positive (got %d)", s->Hkv);
+    if (s->Hq != 16 * s->Hkv)
+        return fail(DVATTN_ERR_UNSUPPORTED, "only GQA 16 is implemented (Hq=%d, Hkv=%d)", s->Hq, s->Hkv);
+    if (s->E != 128 || s->Ev != 128)
+        return fail(DVATTN_ERR_UNSUPPORTED, "only head dims E == Ev == 128 are implemented (E=%d, Ev=%d)", s->E,
+                    s->Ev);
+    return DVATTN_OK;
+}
+
+dvattn_status check_rotary(int R, int E) {
+    if (R < 0 || R > E || (R & 1))
+        return fail(DVATTN_ERR_UNSUPPORTED, "rotary_dim must be even and in [0, E] (got %d, E=%d)", R, E);
+    return DVATTN_OK;
+}
+
+dvattn_status check_pages(const dvattn_shape* s) {
+    if (s->block_size <= 0) return fail(DVATTN_ERR_INVALID, "block_size must be positive (got %d)", s->block_size);
+    if (s->max_blocks_per_seq < 0 || s->num_blocks < 0)
+        return fail(DVATTN_ERR_INVALID, "max_blocks_per_seq / num_blocks must be >= 0");
+    return DVATTN_OK;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+size_t contig_table_bytes(int F) {
+    return F > dv::kMaxFragArgs ? align256((size_t)F * sizeof(dv::FragDesc)) : 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* dvattn_last_error(void) { return g_err; }
+
+int dvattn_abi_version(void) { return DVATTN_ABI_VERSION; }
+
+// ---------------------------------------------------------------------------
+size_t dvattn_paged_sdpa_workspace_size(int dtype, const dvattn_shape* s, int device) {
+    if (!s || !valid_dtype(dtype)) return 0;
+    return dv::decode_workspace_bytes(s->W * s->S, s->Hkv, current_device(device), dtype);
+}
+
+dvattn_status dvattn_paged_sdpa(int dtype, void* out, float scale, const int* locations, const void* queries,
+                                const float* cosines, const float* sines, const int* fragment_lengths,
+                                const void* k_cache, const void* v_cache, const int* block_tables,
+                                const dvattn_shape* s, void* workspace, size_t workspace_bytes, void* stream) {
+    if (!s) return fail(DVATTN_ERR_INVALID, "shape is null");
+    if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+    if (s->F < 0 || s->W < 0 || s->S < 0) return fail(DVATTN_ERR_INVALID, "negative F/W/S");
+    if ((long long)s->W * s->S == 0 || s->Hkv == 0) return ok();  // paged_kernel_v21.cuh:385-386
+    dvattn_status st;
+    if ((st = check_heads(s)) != DVATTN_OK) return st;
+    if ((st = check_rotary(s->rotary_dim, s->E)) != DVATTN_OK) return st;
+    if ((st = check_pages(s)) != DVATTN_OK) return st;
+    if (!out || !queries) return fail(DVATTN_ERR_INVALID, "null output or query pointer");
+    if (s->F > 0 && (!locations || !fragment_lengths || ((!cosines || !sines) && s->rotary_dim > 0)))
+        return fail(DVATTN_ERR_INVALID, "null locations / fragment_lengths / cos / sin pointer");
+    if (s->num_blocks > 0 && (!k_cache || !v_cache)) return fail(DVATTN_ERR_INVALID, "null k/v cache pointer");
+    if (s->max_blocks_per_seq > 0 && !block_tables) return fail(DVATTN_ERR_INVALID, "null block_tables pointer");
+    const size_t need = dvattn_paged_sdpa_workspace_size(dtype, s, -1);
+    if (workspace_bytes < need || (need && !workspace))
+        return fail(DVATTN_ERR_WORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+
+    dv::DecodeParams p;
+    memset(&p, 0, sizeof(p));
+    p.out = out;
+    p.loc = locations;
+    p.q = queries;
+    p.cosv = cosines;
+    p.sinv = sines;
+    p.fl = fragment_lengths;
+    p.kc = k_cache;
+    p.vc = v_cache;
+    p.bt = block_tables;
+    p.l2scale = scale * 1.4426950408889634f;  // scale / ln 2 (paged_kernel_v21.cuh:47)
+    p.F = s->F;
+    p.W = s->W;
+    p.S = s->S;
+    p.Hq = s->Hq;
+    p.Hkv = s->Hkv;
+    p.R = s->rotary_dim;
+    p.bs = s->block_size;
+    p.bs_shift = log2_exact(s->block_size);
+    p.maxB = s->max_blocks_per_seq;
+    p.nblocks = s->num_blocks;
+    p.min_keys = 128;
+    const long long max_keys = (long long)s->max_blocks_per_seq * s->block_size;
+    hipError_t e = dv::launch_decode(dtype, dv::kQRotFull, dv::kKvPaged, dv::kRowWS, p, s->W * s->S, max_keys,
+                                     workspace, workspace_bytes, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dvattn_paged_sdpa launch");
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+size_t dvattn_varlen_paged_sdpa_workspace_size(int dtype, const dvattn_shape* s, int device) {
+    if (!s || !valid_dtype(dtype)) return 0;
+    return dv::decode_workspace_bytes(s->total_q_tokens, s->Hkv, current_device(device), dtype);
+}
+
+dvattn_status dvattn_varlen_paged_sdpa(int dtype, void* out, float scale, const int* locations,
+                                       const void* queries, const float* cosines, const float* sines,
+                                       const int* fragment_lengths, const void* k_cache, const void* v_cache,
+                                       const int* block_tables, const int* cu_seqlens_q, const int* cu_seqlens_k,
+                                       const dvattn_shape* s, void* workspace, size_t workspace_bytes,
+                                       void* stream) {
+    (void)cu_seqlens_k;  // passed but never read by the reference (binding.cu:279,290)
+    if (!s) return fail(DVATTN_ERR_INVALID, "shape is null");
+    if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+    if (s->F < 0 || s->W < 0 || s->total_q_tokens < 0) return fail(DVATTN_ERR_INVALID, "negative F/W/T");
+    if (s->total_q_tokens == 0 || s->Hkv == 0) return ok();  // varlen_paged_kernel_v21.cuh:382-383
+    dvattn_status st;
+    if ((st = check_heads(s)) != DVATTN_OK) return st;
+    if ((st = check_rotary(s->rotary_dim, s->E)) != DVATTN_OK) return st;
+    if ((st = check_pages(s)) != DVATTN_OK) return st;
+    if (!out || !queries) return fail(DVATTN_ERR_INVALID, "null output or query pointer");
+    if (s->W > 0 && !cu_seqlens_q) return fail(DVATTN_ERR_INVALID, "null cu_seqlens_q pointer");
+    if (s->F > 0 && (!locations || !fragment_lengths || ((!cosines || !sines) && s->rotary_dim > 0)))
+        return fail(DVATTN_ERR_INVALID, "null locations / fragment_lengths / cos / sin pointer");
+    if (s->num_blocks > 0 && (!k_cache || !v_cache)) return fail(DVATTN_ERR_INVALID, "null k/v cache pointer");
+    if (s->max_blocks_per_seq > 0 && !block_tables) return fail(DVATTN_ERR_INVALID, "null block_tables pointer");
+    const size_t need = dvattn_varlen_paged_sdpa_workspace_size(dtype, s, -1);
+    if (workspace_bytes < need || (need && !workspace))
+        return fail(DVATTN_ERR_WORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+
+    dv::DecodeParams p;
+    memset(&p, 0, sizeof(p));
+    p.out = out;
+    p.loc = locations;
+    p.q = queries;
+    p.cosv = cosines;
+    p.sinv = sines;
+    p.fl = fragment_lengths;
+    p.kc = k_cache;
+    p.vc = v_cache;
+    p.bt = block_tables;
+    p.cu_q = cu_seqlens_q;
+    p.l2scale = scale * 1.4426950408889634f;
+    p.F = s->F;
+    p.W = s->W;
+    p.S = 1;
+    p.T = s->total_q_tokens;
+    p.Hq = s->Hq;
+    p.Hkv = s->Hkv;
+    p.R = s->rotary_dim;
+    p.bs = s->block_size;
+    p.bs_shift = log2_exact(s->block_size);
+    p.maxB = s->max_blocks_per_seq;
+    p.nblocks = s->num_blocks;
+    p.min_keys = 128;
+    const long long max_keys = (long long)s->max_blocks_per_seq * s->block_size;
+    hipError_t e = dv::launch_decode(dtype, dv::kQRotHalf, dv::kKvPaged, dv::kRowVarlen, p, s->total_q_tokens,
+                                     max_keys, workspace, workspace_bytes, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dvattn_varlen_paged_sdpa launch");
+    return ok();
+}
+
+// ---------------------------------------------------------------------------
+size_t dvattn_sdpa_workspace_size(int dtype, const dvattn_shape* s, int device) {
+    if (!s || !valid_dtype(dtype)) return 0;
+    return dv::decode_workspace_bytes(s->W * s->S, s->Hkv, current_device(device), dtype) +
+           contig_table_bytes(s->F);
+}
+
+dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* locations, const void* rotated_queries,
+                          const int* fragment_lengths, const void* const* key_fragments,
+                          const void* const* value_fragments, const int* fragment_tokens,
+                          const int* fragment_batch, const dvattn_shape* s, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    if (!s) return fail(DVATTN_ERR_INVALID, "shape is null");
+    if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+    if (s->F < 0 || s->W < 0 || s->S < 0) return fail(DVATTN_ERR_INVALID, "negative F/W/S");
+    if ((long long)s->W * s->S == 0 || s->Hkv == 0) return ok();
+    dvattn_status st;
+    if ((st = check_heads(s)) != DVATTN_OK) return st;
+    if (!out || !rotated_queries) return fail(DVATTN_ERR_INVALID, "null output or query pointer");
+    if (s->F > 0 && (!locations || !fragment_lengths || !key_fragments || !value_fragments || !fragment_tokens ||
+                     !fragment_batch))
+        return fail(DVATTN_ERR_INVALID, "null locations / fragment_lengths / fragment arrays");
+    const size_t need = dvattn_sdpa_workspace_size(dtype, s, -1);
+    if (workspace_bytes < need || (need && !workspace))
+        return fail(DVATTN_ERR_WORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
+
+    dv::DecodeParams p;
+    memset(&p, 0, sizeof(p));
+    const size_t tab_bytes = contig_table_bytes(s->F);
+    std::vector<dv::FragDesc> tab((size_t)s->F);
+    long long max_keys = 0;
+    const size_t esz = dtype == DVATTN_F32 ? 4 : 2;
+    for (int f = 0; f < s->F; ++f) {
+        const int L = fragment_tokens[f];
+        const int B = fragment_batch[f];
+        if (L < 0) return fail(DVATTN_ERR_INVALID, "fragment %d: negative token count", f);
+        if (B != 1 && B != s->W)
+            return fail(DVATTN_ERR_INVALID, "fragment %d: batch %d is neither 1 nor W=%d", f, B, s->W);
+        if (L > 0 && (!key_fragments[f] || !value_fragments[f]))
+            return fail(DVATTN_ERR_INVALID, "fragment %d: null pointer", f);
+        if ((((uintptr_t)key_fragments[f]) | ((uintptr_t)value_fragments[f])) & 15)
+            return fail(DVATTN_ERR_INVALID, "fragment %d: pointers must be 16-byte aligned", f);
+        dv::FragDesc& d = tab[(size_t)f];
+        d.k = key_fragments[f];
+        d.v = value_fragments[f];
+        d.L = L;
+        d.bstride = B == 1 ? 0 : (long long)s->Hkv * L * 128;
+        d.pad = 0;
+        max_keys += L;
+        if (f < dv::kMaxFragArgs) p.frags[f] = d;
+    }
+    (void)esz;
+    void* ws = workspace;
+    size_t ws_left = workspace_bytes;
+    if (tab_bytes) {
+        hipError_t e = hipMemcpyAsync(workspace, tab.data(), (size_t)s->F * sizeof(dv::FragDesc),
+                                      hipMemcpyHostToDevice, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa fragment table upload");
+        p.frag_tab = reinterpret_cast<const dv::FragDesc*>(workspace);
+        ws = reinterpret_cast<unsigned char*>(workspace) + tab_bytes;
+        ws_left -= tab_bytes;
+    }
+    p.out = out;
+    p.loc = locations;
+    p.q = rotated_queries;
+    p.fl = fragment_lengths;
+    p.l2scale = scale * 1.4426950408889634f;
+    p.F = s->F;
+    p.W = s->W;
+    p.S = s->S;
+    p.Hq = s->Hq;
+    p.Hkv = s->Hkv;
+    p.R = 0;
+    p.bs = 1;
+    p.bs_shift = 0;
+    p.min_keys = 128;
+    hipError_t e = dv::launch_decode(dtype, dv::kQPre, dv::kKvContig, dv::kRowWS, p, s->W * s->S, max_keys, ws,
+                                     ws_left, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa launch");
+    return ok();
+}
+
+dvattn_status dvattn_fused(int dtype, void* out, void* rotated_queries, float scale, const int* locations,
+                           const void* queries, const int* fragment_lengths, const void* const* key_fragments,
+                           const void* const* value_fragments, const int* fragment_tokens,
+                           const int* fragment_batch, const float* cosines, const float* sines,
+                           const dvattn_shape* s, void* workspace, size_t workspace_bytes, void* stream) {
+    dvattn_status st = dvattn_rope(dtype, rotated_queries, queries, cosines, sines, s, stream);
+    if (st != DVATTN_OK) return st;
+    return dvattn_sdpa(dtype, out, scale, locations, rotated_queries, fragment_lengths, key_fragments,
+                       value_fragments, fragment_tokens, fragment_batch, s, workspace, workspace_bytes, stream);
+}
+
+// ---------------------------------------------------------------------------
+dvattn_status dvattn_rope(int dtype, void* out, const void* queries, const float* cosines, const float* sines,
+                          const dvattn_shape* s, void* stream) {
+    if (!s) return fail(DVATTN_ERR_INVALID, "shape is null");
+    if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+    if (s->F < 0 || s->W < 0 || s->Hq < 0 || s->S < 0 || s->E < 0)
+        return fail(DVATTN_ERR_INVALID, "negative size");
+    dvattn_status st;
+    if ((st = check_rotary(s->rotary_dim, s->E)) != DVATTN_OK) return st;
+    if ((long long)s->F * s->W * s->Hq * s->S * s->E == 0) return ok();  // rope.cuh:58-60
+    if (!out || !queries || (s->rotary_dim > 0 && (!cosines || !sines)))
+        return fail(DVATTN_ERR_INVALID, "null pointer");
+    dv::RopeParams p;
+    memset(&p, 0, sizeof(p));
+    p.out = out;
+    p.q = queries;
+    p.cosv = cosines;
+    p.sinv = sines;
+    p.F = s->F;
+    p.W = s->W;
+    p.Hq = s->Hq;
+    p.S = s->S;
+    p.E = s->E;
+    p.R = s->rotary_dim;
+    p.half_width = 0;
+    hipError_t e = dv::launch_rope(dtype, p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dvattn_rope launch");
+    return ok();
+}
+
+dvattn_status dvattn_varlen_rope(int dtype, void* out, const void* queries, const float* cosines,
+                                 const float* sines, const dvattn_shape* s, void* stream) {
+    if (!s) return fail(DVATTN_ERR_INVALID, "shape is null");
+    if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+    if (s->F < 0 || s->total_q_tokens < 0 || s->Hq < 0 || s->E < 0) return fail(DVATTN_ERR_INVALID, "negative size");
+    dvattn_status st;
+    if ((st = check_rotary(s->rotary_dim, s->E)) != DVATTN_OK) return st;
+    if ((long long)s->F * s->total_q_tokens * s->Hq * s->E == 0) return ok();  // rope.cuh:106-108
+    if (!out || !queries || (s->rotary_dim > 0 && (!cosines || !sines)))
+        return fail(DVATTN_ERR_INVALID, "null pointer");
+    dv::RopeParams p;
+    memset(&p, 0, sizeof(p));
+    p.out = out;
+    p.q = queries;
+    p.cosv = cosines;
+    p.sinv = sines;
+    p.F = s->F;
+    p.T = s->total_q_tokens;
+    p.Hq = s->Hq;
+    p.E = s->E;
+    p.R = s->rotary_dim;
+    p.half_width = 1;
+    hipError_t e = dv::launch_rope(dtype, p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dvattn_varlen_rope launch");
+    return ok();
+}
+
+}  // extern "C"

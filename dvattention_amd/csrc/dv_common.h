@@ -1,0 +1,95 @@
+// Shared host/device definitions of the gfx950 DVAttn kernels: compile-time
+// limits, the launch-parameter structs passed by value to the kernels, and the
+// internal launcher API used by the C ABI layer (dv_capi.hip).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace dv {
+
+constexpr int kWave = 64;         // CDNA wavefront width
+constexpr int kGqa = 16;          // query heads per KV head (reference hard-wires 16)
+constexpr int kHeadDim = 128;     // E == Ev == 128 (reference hard-wires 128)
+constexpr int kStep = 32;         // keys per wave per pipeline step (two 16-key MFMA blocks)
+constexpr int kMaxRows = 4096;    // query rows per decode launch (schedule prefix lives in LDS)
+constexpr int kMaxFragArgs = 16;  // contiguous views passed in kernel arguments
+constexpr int kMaxWavesPerWg = 4; // KV heads per workgroup (one wave per KV head)
+
+// Storage dtype codes (same values as dvattn_dtype in include/dvattn_amd.h).
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+// How the query of (row, view) is obtained.
+enum QMode : int {
+    kQRotFull = 0,  // rotate queries [W,Hq,S,E] with full-width cos/sin [F,W,S,R]
+    kQRotHalf = 1,  // rotate queries [T,Hq,E] with half-width cos/sin [F,T,R/2]
+    kQPre = 2       // read rotated queries [F,W,Hq,S,E]
+};
+
+// Where the keys/values of (sequence, view, token) live.
+enum KvMode : int {
+    kKvPaged = 0,   // [num_blocks, block_size, Hkv, E] pages via block_tables
+    kKvContig = 1   // per-view [B, Hkv, L, E] tensors
+};
+
+// How a query row maps to a sequence / query token.
+enum RowMode : int {
+    kRowWS = 0,     // row r = w*S + s
+    kRowVarlen = 1  // row r = packed token t, sequence from cu_seqlens_q
+};
+
+struct FragDesc {
+    const void* k;        // [B, Hkv, L, E]
+    const void* v;        // [B, Hkv, L, Ev]
+    long long bstride;    // elements between batch entries (0: one batch shared by all rows)
+    int L;                // tokens in the tensor
+    int pad;
+};
+
+struct DecodeParams {
+    void* out;
+    float* part;          // partial results, slot-major: [slot][hpw*16][Ev] then [slot][hpw*16] lse
+    int* dir;             // per (row, head-group) segment: {first slot, piece count}
+    const int* loc;
+    const void* q;
+    const float* cosv;
+    const float* sinv;
+    const int* fl;        // fragment_lengths [F] (device)
+    const void* kc;
+    const void* vc;
+    const int* bt;
+    const int* cu_q;
+    const FragDesc* frag_tab;  // device table when F > kMaxFragArgs
+    float l2scale;        // softmax scale / ln(2): scores are kept in base-2 units
+    int F, W, S, Hq, Hkv, R;
+    int bs, bs_shift, maxB, nblocks;
+    int T;
+    int row_begin, nrows;
+    int hpw;              // KV heads (waves) per workgroup
+    int nwg;              // workgroups launched
+    int min_keys;         // smallest key range worth a workgroup
+    int slot_floats;      // floats per partial slot
+    FragDesc frags[kMaxFragArgs];
+};
+
+struct RopeParams {
+    void* out;
+    const void* q;
+    const float* cosv;
+    const float* sinv;
+    int F, W, Hq, S, E, R;
+    int T;                // varlen
+    int half_width;       // 1: cos/sin rows hold R/2 entries (varlen layout)
+};
+
+// Internal launchers (return a hipError_t; argument validation happens in the C ABI).
+size_t decode_workspace_bytes(int nrows_total, int Hkv, int device, int dtype);
+// max_keys_per_row: host-known upper bound of the visible keys of one row (sizes
+// the grid for small problems).
+hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const DecodeParams& base,
+                         int nrows_total, long long max_keys_per_row, void* workspace, size_t ws_bytes,
+                         hipStream_t stream);
+hipError_t launch_rope(int dtype, const RopeParams& p, hipStream_t stream);
+
+}  // namespace dv

@@ -1,0 +1,828 @@
+// gfx950 decode attention with fused query RoPE (paged / varlen / contiguous views).
+//
+// Restates the operator semantics of src/kernels/paged_kernel_v21.cuh:17-374,
+// src/kernels/varlen_paged_kernel_v21.cuh:17-371 and src/kernels/kernel_v21.cuh:17-367
+// (reference repository) with an MI355X-first design:
+//
+//  * One wave owns one KV head and its 16 query heads of one query row, for a
+//    contiguous range of that row's visible keys.  A workgroup holds up to four
+//    such waves (four KV heads of the same row and key range), so a token's K/V
+//    rows for those heads are fetched together.
+//  * Scores are computed transposed on MFMA, S^T = K Q^T (16 keys x 16 heads per
+//    16x16x32 bf16/f16 MFMA, 4 per 16 keys), so every lane owns one query head:
+//    the online softmax needs only two cross-lane reductions per 32 keys and no
+//    layout change.  The output is accumulated transposed too, O^T += V^T P^T,
+//    with P^T taken straight from the score registers and V^T read from a
+//    wave-private LDS tile with the gfx950 transposing LDS read.
+//  * The query of each view is rotated once per (row, view) in registers while
+//    it is loaded (no rotated-query round trip through HBM).
+//  * Work balance: every workgroup computes the same schedule from locations /
+//    fragment_lengths: all (row, KV-head-group) segments of visible keys are laid
+//    end to end and cut into equal contiguous chunks, one per workgroup.  A
+//    segment that one workgroup finishes alone is written straight to the output;
+//    otherwise the pieces go to fp32 partial slots (normalised output + base-2
+//    log-sum-exp) and dv_merge combines them, as the reference's reduce kernels
+//    do (paged_kernel_v21.cuh:307-374).
+#include "dv_common.h"
+#include "dv_device.h"
+
+namespace dv {
+
+constexpr int kVtStride16 = 288;                 // V tile row (bytes), 16-bit types: 256 + 32 pad
+constexpr int kVtStride32 = 528;                 // fp32: 512 + 16 pad
+constexpr int kVtBytes16 = kStep * kVtStride16;  // 9216 B per wave
+constexpr int kVtBytes32 = kStep * kVtStride32;  // 16896 B per wave
+
+template <int DT> constexpr int vt_bytes() { return DT == kF32 ? kVtBytes32 : kVtBytes16; }
+
+// ---- row / view helpers -------------------------------------------------------
+
+template <int RM>
+__device__ inline int row_loc(const DecodeParams& p, int row, int f) {
+    if (RM == kRowVarlen) return p.loc[(long long)f * p.T + row];
+    const int w = row / p.S;
+    const int s = row - w * p.S;
+    return p.loc[((long long)f * p.W + w) * p.S + s];
+}
+
+template <int KVM>
+__device__ inline const FragDesc& frag(const DecodeParams& p, int f) {
+    return f < kMaxFragArgs ? p.frags[f] : p.frag_tab[f];
+}
+
+// Visible keys of view f for a query at location locv:
+// min(L_f, loc + 1) clamped at 0 (paged_kernel_v21.cuh:83-85); varlen views with
+// loc < 0 are skipped (varlen_paged_kernel_v21.cuh:76-80), which is the same count.
+template <int KVM>
+__device__ inline int view_vis(const DecodeParams& p, int f, int locv) {
+    long long L = p.fl[f];
+    if (KVM == kKvContig) L = L < frag<KVM>(p, f).L ? L : frag<KVM>(p, f).L;
+    long long v = (long long)locv + 1;
+    v = v < L ? v : L;
+    return v > 0 ? (int)v : 0;
+}
+
+template <int KVM, int RM>
+__device__ inline long long row_visible(const DecodeParams& p, int row) {
+    long long v = 0;
+    for (int f = 0; f < p.F; ++f) v += view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
+    return v;
+}
+
+// Sequence of packed token t: first i with t < cu_seqlens_q[i+1], else 0
+// (varlen_paged_kernel_v21.cuh:40-47).  Wave-cooperative, 64 entries per ballot.
+__device__ inline int varlen_seq(const DecodeParams& p, int t) {
+    const int lane = threadIdx.x & 63;
+    for (int base = 0; base < p.W; base += kWave) {
+        const int i = base + lane;
+        const bool hit = i < p.W && t < p.cu_q[i + 1];
+        const uint64_t b = ballot(hit);
+        if (b) return base + __builtin_ctzll(b);
+    }
+    return 0;
+}
+
+// ---- per-wave K/V staging -----------------------------------------------------
+
+// Page-table window: lane l holds the physical page of logical page wbase + l.
+struct PageWin {
+    long long wbase;
+    int pg;
+};
+
+struct KvCtx {
+    const unsigned char* k;  // base of this view's K (contig) or the K cache (paged)
+    const unsigned char* v;
+    long long off;           // paged: logical position of the view's first token
+    long long bstride;       // contig: element offset of this row's batch entry
+    int L;                   // contig: tokens in the fragment tensor
+    int w;
+    int hkv;
+};
+
+template <int DT, int KVM>
+__device__ inline void window_update(const DecodeParams& p, const KvCtx& c, PageWin& win, int l, int l1) {
+    if (KVM != kKvPaged) return;
+    const long long pf = c.off + l;
+    const long long plast = c.off + (l + kStep - 1 < l1 - 1 ? l + kStep - 1 : l1 - 1);
+    long long lpf, lpl;
+    if (p.bs_shift >= 0) {
+        lpf = pf >> p.bs_shift;
+        lpl = plast >> p.bs_shift;
+    } else {
+        lpf = pf >= 0 ? pf / p.bs : -((-pf + p.bs - 1) / p.bs);
+        lpl = plast >= 0 ? plast / p.bs : -((-plast + p.bs - 1) / p.bs);
+    }
+    if (lpf >= win.wbase && lpl < win.wbase + kWave) return;
+    win.wbase = lpf;
+    const long long lp = lpf + (threadIdx.x & 63);
+    win.pg = (lp >= 0 && lp < p.maxB) ? p.bt[(long long)c.w * p.maxB + lp] : -1;
+}
+
+// Element offset (same for K and V since E == Ev) of the row holding key `key`
+// of the current view, or -1 if the key is not visible / not addressable.
+template <int KVM>
+__device__ inline long long kv_row(const DecodeParams& p, const KvCtx& c, const PageWin& win,
+                                   int key, int l1) {
+    if (KVM == kKvPaged) {
+        const long long pos = c.off + key;
+        long long lp, r;
+        if (p.bs_shift >= 0) {
+            lp = pos >> p.bs_shift;
+            r = pos - (lp << p.bs_shift);
+        } else {
+            lp = pos >= 0 ? pos / p.bs : -((-pos + p.bs - 1) / p.bs);
+            r = pos - lp * p.bs;
+        }
+        const long long idx = lp - win.wbase;
+        const int page = shfl_i(win.pg, (int)(idx & 63));
+        const bool ok = key < l1 && idx >= 0 && idx < kWave && lp < p.maxB && page >= 0 && page < p.nblocks;
+        const long long off = (((long long)page * p.bs + r) * p.Hkv + c.hkv) * kHeadDim;
+        return ok ? off : -1;
+    } else {
+        const long long off = c.bstride + ((long long)c.hkv * c.L + key) * kHeadDim;
+        return key < l1 ? off : -1;
+    }
+}
+
+// 16-bit types: one step = keys [l, l+32) as two 16-key MFMA blocks.
+// Lane (g = lane/16, m = lane%16) loads dims [c*32 + g*8, +8), c = 0..3, of keys
+// m and 16+m: the A operand of S^T = K Q^T, and the V rows it stages in LDS.
+struct Kv16 {
+    u32x4 k[2][4];
+    u32x4 v[2][4];
+    uint32_t mask;  // bit j: key l+j visible
+};
+
+// Rows of zeros that invisible keys load from, so every lane issues the same
+// loads (no divergent branches around the memory instructions).
+__device__ __align__(16) unsigned char g_zero_row[512];
+
+template <int DT, int KVM>
+__device__ inline void issue16(const DecodeParams& p, const KvCtx& c, const PageWin& win, Kv16& b,
+                               int l, int l1) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, m = lane & 15;
+    bool okb[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        const long long row = kv_row<KVM>(p, c, win, l + kb * 16 + m, l1);
+        okb[kb] = row >= 0;
+        const unsigned char* kp = okb[kb] ? c.k + (row + g * 8) * 2 : g_zero_row + g * 16;
+        const unsigned char* vp = okb[kb] ? c.v + (row + g * 8) * 2 : g_zero_row + g * 16;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) b.k[kb][cc] = ld16(kp + cc * 64);
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) b.v[kb][cc] = ld16(vp + cc * 64);
+    }
+    b.mask = (uint32_t)(ballot(okb[0]) & 0xffffu) | ((uint32_t)(ballot(okb[1]) & 0xffffu) << 16);
+}
+
+struct SoftState {
+    f32x4 o[8];   // O^T: lane (g, n) holds dims c*16 + g*4 + i of head n
+    float m;      // running max of base-2 scores (same in the 4 lane groups)
+    float l;      // this lane's partial sum of exp2(score - m)
+};
+
+// Online softmax update for one step, given the two 16-key S^T blocks.
+// Returns the unnormalised probabilities (8 per lane) in pr.
+__device__ inline void softmax_step(SoftState& st, const f32x4& s0, const f32x4& s1, uint32_t mask,
+                                    float l2scale, float (&pr)[8]) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    float t[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        t[i] = ((mask >> (g * 4 + i)) & 1u) ? s0[i] * l2scale : -DV_INF;
+        t[4 + i] = ((mask >> (16 + g * 4 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
+    }
+    float mx = t[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, t[i]);
+    mx = fmaxf(mx, shfl_xor_f(mx, 16));
+    mx = fmaxf(mx, shfl_xor_f(mx, 32));
+    const float mnew = fmaxf(st.m, mx);
+    float alpha;
+    if (mnew == -DV_INF) {
+        alpha = 1.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = 0.0f;
+    } else {
+        alpha = exp2f(st.m - mnew);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = exp2f(t[i] - mnew);
+    }
+    float ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ps += pr[i];
+    st.l = st.l * alpha + ps;
+    st.m = mnew;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) st.o[c] *= alpha;
+}
+
+template <int DT>
+__device__ inline void compute16(SoftState& st, const Kv16& b, const u32x4 (&qB)[4], unsigned char* vt,
+                                 float l2scale) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, m = lane & 15;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        s0 = Tr<DT>::mma(b.k[0][cc], qB[cc], s0);
+        s1 = Tr<DT>::mma(b.k[1][cc], qB[cc], s1);
+    }
+    // stage V rows: key kb*16+m, bytes [c*64 + g*16, +16)
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc)
+            *reinterpret_cast<u32x4*>(vt + (kb * 16 + m) * kVtStride16 + cc * 64 + g * 16) = b.v[kb][cc];
+    compiler_fence();
+    float pr[8];
+    softmax_step(st, s0, s1, b.mask, l2scale, pr);
+    // P^T operand: k = g*8 + jj <-> key (jj/4)*16 + g*4 + jj%4
+    const u32x4 pB = {pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]),
+                      pack2<DT>(pr[6], pr[7])};
+    // V^T operand for dims [c*16, +16): block lane sl points at key g*4 + sl/4,
+    // dims c*16 + (sl%4)*4; the transposed read hands lane n V[g*4+j][c*16+n].
+    const int sl = lane & 15;
+    const unsigned char* vbase = vt + (g * 4 + (sl >> 2)) * kVtStride16 + (sl & 3) * 8;
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) {
+        const u32x2 a0 = lds_read_tr16(vbase + cc * 32);
+        const u32x2 a1 = lds_read_tr16(vbase + 16 * kVtStride16 + cc * 32);
+        const u32x4 vA = {a0[0], a0[1], a1[0], a1[1]};
+        st.o[cc] = Tr<DT>::mma(vA, pB, st.o[cc]);
+    }
+    compiler_fence();
+}
+
+// fp32: lane (g, m) loads dims [c*16 + g*4, +4), c = 0..7, of keys m and 16+m.
+struct Kv32 {
+    f32x4 k[2][8];
+    f32x4 v[2][8];
+    uint32_t mask;
+};
+
+template <int KVM>
+__device__ inline void issue32(const DecodeParams& p, const KvCtx& c, const PageWin& win, Kv32& b,
+                               int l, int l1) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, m = lane & 15;
+    bool okb[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+        const long long row = kv_row<KVM>(p, c, win, l + kb * 16 + m, l1);
+        okb[kb] = row >= 0;
+        const unsigned char* kp = okb[kb] ? c.k + (row + g * 4) * 4 : g_zero_row + g * 16;
+        const unsigned char* vp = okb[kb] ? c.v + (row + g * 4) * 4 : g_zero_row + g * 16;
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) b.k[kb][cc] = ld16f(kp + cc * 64);
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) b.v[kb][cc] = ld16f(vp + cc * 64);
+    }
+    b.mask = (uint32_t)(ballot(okb[0]) & 0xffffu) | ((uint32_t)(ballot(okb[1]) & 0xffffu) << 16);
+}
+
+__device__ inline void compute32(SoftState& st, const Kv32& b, const f32x4 (&qB)[8], unsigned char* vt,
+                                 float l2scale) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, m = lane & 15, n = lane & 15;
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            s0 = Tr<kF32>::mma1(b.k[0][cc][j], qB[cc][j], s0);
+            s1 = Tr<kF32>::mma1(b.k[1][cc][j], qB[cc][j], s1);
+        }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc)
+            *reinterpret_cast<f32x4*>(vt + (kb * 16 + m) * kVtStride32 + (cc * 16 + g * 4) * 4) = b.v[kb][cc];
+    compiler_fence();
+    float pr[8];
+    softmax_step(st, s0, s1, b.mask, l2scale, pr);
+    // O^T += V^T P^T, 4 keys per MFMA: k = g <-> key kb*16 + g*4 + i
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float* vrow = reinterpret_cast<const float*>(vt + (kb * 16 + g * 4 + i) * kVtStride32);
+            const float pb = pr[kb * 4 + i];
+#pragma unroll
+            for (int cc = 0; cc < 8; ++cc) st.o[cc] = Tr<kF32>::mma1(vrow[cc * 16 + n], pb, st.o[cc]);
+        }
+    compiler_fence();
+}
+
+// ---- query operand ------------------------------------------------------------
+
+// 16-bit: lane (g, n) holds Q[n][c*32 + g*8 + 0..7] for c = 0..3 (B operand of S^T).
+template <int DT, int QM, int RM>
+__device__ inline void load_q16(const DecodeParams& p, int row, int f, int hkv, u32x4 (&qB)[4]) {
+    using raw = typename Tr<DT>::raw;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    const int h = hkv * kGqa + n;
+    if (QM == kQPre) {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        const raw* q = reinterpret_cast<const raw*>(p.q) +
+                       ((((long long)f * p.W + w) * p.Hq + h) * p.S + s) * kHeadDim;
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) qB[cc] = ld16(q + cc * 32 + g * 8);
+        return;
+    }
+    const raw* q;
+    const float* cs;
+    const float* sn;
+    if (QM == kQRotFull) {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        q = reinterpret_cast<const raw*>(p.q) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+        const long long co = (((long long)f * p.W + w) * p.S + s) * p.R;
+        cs = p.cosv + co;
+        sn = p.sinv + co;
+    } else {
+        q = reinterpret_cast<const raw*>(p.q) + ((long long)row * p.Hq + h) * kHeadDim;
+        const long long co = ((long long)f * p.T + row) * (p.R >> 1);
+        cs = p.cosv + co;
+        sn = p.sinv + co;
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        raw r[8];
+        rotate_run<DT, 8>(q, cs, sn, p.R, cc * 32 + g * 8, r);
+        qB[cc] = u32x4{(uint32_t)r[0] | ((uint32_t)r[1] << 16), (uint32_t)r[2] | ((uint32_t)r[3] << 16),
+                       (uint32_t)r[4] | ((uint32_t)r[5] << 16), (uint32_t)r[6] | ((uint32_t)r[7] << 16)};
+    }
+}
+
+// fp32: lane (g, n) holds Q[n][c*16 + g*4 + 0..3] for c = 0..7.
+template <int QM, int RM>
+__device__ inline void load_q32(const DecodeParams& p, int row, int f, int hkv, f32x4 (&qB)[8]) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    const int h = hkv * kGqa + n;
+    if (QM == kQPre) {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        const float* q = reinterpret_cast<const float*>(p.q) +
+                         ((((long long)f * p.W + w) * p.Hq + h) * p.S + s) * kHeadDim;
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) qB[cc] = ld16f(q + cc * 16 + g * 4);
+        return;
+    }
+    const float* q;
+    const float* cs;
+    const float* sn;
+    if (QM == kQRotFull) {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        q = reinterpret_cast<const float*>(p.q) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+        const long long co = (((long long)f * p.W + w) * p.S + s) * p.R;
+        cs = p.cosv + co;
+        sn = p.sinv + co;
+    } else {
+        q = reinterpret_cast<const float*>(p.q) + ((long long)row * p.Hq + h) * kHeadDim;
+        const long long co = ((long long)f * p.T + row) * (p.R >> 1);
+        cs = p.cosv + co;
+        sn = p.sinv + co;
+    }
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) {
+        float r[4];
+        rotate_run<kF32, 4>(q, cs, sn, p.R, cc * 16 + g * 4, r);
+        qB[cc] = f32x4{r[0], r[1], r[2], r[3]};
+    }
+}
+
+// ---- one wave: one KV head over visible keys [v0, v1) of one row ---------------
+
+template <int DT, int QM, int KVM, int RM>
+__device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row, int hkv, long long v0,
+                              long long v1, bool final_out, int slot, int wv) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+
+    int w;
+    if (RM == kRowVarlen) w = varlen_seq(p, row);
+    else w = row / p.S;
+
+    SoftState st;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = -DV_INF;
+    st.l = 0.0f;
+
+    PageWin win;
+    win.wbase = -(1ll << 60);
+    win.pg = -1;
+
+    long long P = 0;    // visible keys of the earlier views
+    long long off = 0;  // logical position of view f (paged): sum of earlier fragment_lengths
+    for (int f = 0; f < p.F && P < v1; ++f) {
+        const int vis = view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
+        const long long a = v0 > P ? v0 : P;
+        const long long bnd = v1 < P + vis ? v1 : P + vis;
+        if (a < bnd) {
+            const int l0 = (int)(a - P), l1 = (int)(bnd - P);
+            KvCtx c;
+            c.w = w;
+            c.hkv = hkv;
+            if (KVM == kKvPaged) {
+                c.k = reinterpret_cast<const unsigned char*>(p.kc);
+                c.v = reinterpret_cast<const unsigned char*>(p.vc);
+                c.off = off;
+                c.bstride = 0;
+                c.L = 0;
+            } else {
+                const FragDesc& fd = frag<KVM>(p, f);
+                c.k = reinterpret_cast<const unsigned char*>(fd.k);
+                c.v = reinterpret_cast<const unsigned char*>(fd.v);
+                c.off = 0;
+                c.bstride = fd.bstride * w;
+                c.L = fd.L;
+            }
+            if constexpr (DT == kF32) {
+                f32x4 qB[8];
+                load_q32<QM, RM>(p, row, f, hkv, qB);
+                for (int l = l0; l < l1; l += kStep) {
+                    Kv32 b;
+                    window_update<DT, KVM>(p, c, win, l, l1);
+                    issue32<KVM>(p, c, win, b, l, l1);
+                    compute32(st, b, qB, vt, p.l2scale);
+                }
+            } else {
+                u32x4 qB[4];
+                load_q16<DT, QM, RM>(p, row, f, hkv, qB);
+                Kv16 b0, b1;
+                window_update<DT, KVM>(p, c, win, l0, l1);
+                issue16<DT, KVM>(p, c, win, b0, l0, l1);
+                for (int l = l0; l < l1; l += 2 * kStep) {
+                    const bool has1 = l + kStep < l1;
+                    if (has1) {
+                        window_update<DT, KVM>(p, c, win, l + kStep, l1);
+                        issue16<DT, KVM>(p, c, win, b1, l + kStep, l1);
+                    }
+                    compute16<DT>(st, b0, qB, vt, p.l2scale);
+                    if (!has1) break;
+                    if (l + 2 * kStep < l1) {
+                        window_update<DT, KVM>(p, c, win, l + 2 * kStep, l1);
+                        issue16<DT, KVM>(p, c, win, b0, l + 2 * kStep, l1);
+                    }
+                    compute16<DT>(st, b1, qB, vt, p.l2scale);
+                }
+            }
+        }
+        P += vis;
+        off += p.fl[f];
+    }
+
+    // epilogue: total over the four lane groups, normalise, base-2 LSE
+    float lt = st.l + shfl_xor_f(st.l, 16);
+    lt += shfl_xor_f(lt, 32);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const int h = hkv * kGqa + n;
+    if (final_out) {
+        using raw = typename Tr<DT>::raw;
+        raw* o;
+        if (RM == kRowVarlen) {
+            o = reinterpret_cast<raw*>(p.out) + ((long long)row * p.Hq + h) * kHeadDim;
+        } else {
+            const int s = row - w * p.S;
+            o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int d = c * 16 + g * 4;
+            if constexpr (DT == kF32) {
+                *reinterpret_cast<f32x4*>(o + d) = st.o[c] * inv;
+            } else {
+                const u32x2 pk = {pack2<DT>(st.o[c][0] * inv, st.o[c][1] * inv),
+                                  pack2<DT>(st.o[c][2] * inv, st.o[c][3] * inv)};
+                *reinterpret_cast<u32x2*>(o + d) = pk;
+            }
+        }
+    } else {
+        float* sbase = p.part + (long long)slot * p.slot_floats;
+        float* o = sbase + (wv * kGqa + n) * kHeadDim;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(o + c * 16 + g * 4) = st.o[c] * inv;
+        if (g == 0) {
+            sbase[p.hpw * kGqa * kHeadDim + wv * kGqa + n] = lt > 0.0f ? st.m + log2f(lt) : -DV_INF;
+        }
+    }
+}
+
+// ---- the decode kernel ----------------------------------------------------------
+
+template <int DT, int QM, int KVM, int RM>
+__global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ long long s_scan[4];
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6;
+    const int nthreads = blockDim.x;
+    const int HPW = p.hpw;
+    const int NHG = p.Hkv / HPW;
+    long long* s_pref = reinterpret_cast<long long*>(smem + HPW * vt_bytes<DT>());
+
+    // 1. per-row visible key counts -> exclusive prefix sums in LDS
+    const int nrows = p.nrows;
+    const int per = (nrows + nthreads - 1) / nthreads;
+    const int r0 = tid * per;
+    const int r1 = r0 + per < nrows ? r0 + per : nrows;
+    long long mine = 0;
+    for (int r = r0; r < r1; ++r) mine += row_visible<KVM, RM>(p, p.row_begin + r);
+    // wave inclusive scan
+    const int lane = tid & 63;
+    long long incl = mine;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const long long o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) s_scan[wv] = incl;
+    __syncthreads();
+    long long before = 0;
+    for (int i = 0; i < wv; ++i) before += s_scan[i];
+    long long run = before + incl - mine;
+    for (int r = r0; r < r1; ++r) {
+        s_pref[r] = run;
+        run += row_visible<KVM, RM>(p, p.row_begin + r);
+    }
+    long long total = 0;
+    for (int i = 0; i < nthreads / kWave; ++i) total += s_scan[i];
+    if (tid == 0) s_pref[nrows] = total;
+    __syncthreads();
+
+    // 2. equal chunks of the (row, head-group) key segments laid end to end
+    const long long Wk = total * NHG;
+    const int geff = Wk == 0 ? 0
+                             : (int)((Wk + p.min_keys - 1) / p.min_keys < p.nwg ? (Wk + p.min_keys - 1) / p.min_keys
+                                                                                : p.nwg);
+    const long long chunk = geff ? (Wk + geff - 1) / geff : 1;
+
+    // directory: segment sg = r*NHG + hg -> {first slot, piece count}
+    if (blockIdx.x == 0) {
+        for (int sg = tid; sg < nrows * NHG; sg += nthreads) {
+            const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
+            const long long V = s_pref[r + 1] - s_pref[r];
+            int base = 0, cnt = 0;
+            if (V > 0) {
+                const long long stt = NHG * s_pref[r] + hg * V;
+                const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
+                cnt = (int)(gl - gf + 1);
+                base = (int)gf + sg;
+            }
+            p.dir[2 * sg] = base;
+            p.dir[2 * sg + 1] = cnt;
+        }
+    }
+    const int gidx = blockIdx.x;
+    if (gidx >= geff) return;
+
+    long long u = gidx * chunk;
+    const long long uend = u + chunk < Wk ? u + chunk : Wk;
+    // last row r with NHG*pref[r] <= u
+    int lo = 0, hi = nrows - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (NHG * s_pref[mid] <= u) lo = mid;
+        else hi = mid - 1;
+    }
+    int r = lo;
+    unsigned char* vt = smem + wv * vt_bytes<DT>();
+    while (u < uend && r < nrows) {
+        const long long rs = NHG * s_pref[r];
+        const long long V = s_pref[r + 1] - s_pref[r];
+        if (V == 0 || u >= rs + NHG * V) {
+            ++r;
+            continue;
+        }
+        const long long rel = u - rs;
+        const int hg = (int)(rel / V);
+        const long long v0 = rel - hg * V;
+        const long long segend = (long long)(hg + 1) * V;
+        const long long lim = (uend - rs < segend ? uend - rs : segend) - (long long)hg * V;
+        const int sg = r * NHG + hg;
+        const long long stt = rs + hg * V;
+        const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
+        const int cnt = (int)(gl - gf + 1);
+        const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
+        if (wv < HPW) {
+            process_piece<DT, QM, KVM, RM>(p, vt, p.row_begin + r, hg * HPW + wv, v0, lim, cnt == 1, slot,
+                                           wv);
+        }
+        u = stt + lim;
+    }
+}
+
+// ---- split merge -------------------------------------------------------------------
+
+// One block per segment (row, head group).  count == 1: already final;
+// count == 0: no visible key -> zeros (paged_kernel_v21.cuh:318); otherwise the
+// LSE-weighted sum of the pieces (paged_kernel_v21.cuh:325-364).
+template <int DT, int RM>
+__global__ __launch_bounds__(256) void dv_merge(const DecodeParams p) {
+    using raw = typename Tr<DT>::raw;
+    const int sg = blockIdx.x;
+    const int NHG = p.Hkv / p.hpw;
+    const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
+    if (cnt == 1) return;
+    const int tid = threadIdx.x;
+    const int j = tid >> 2;  // head within the group
+    if (j >= p.hpw * kGqa) return;
+    const int d0 = (tid & 3) * 32;
+    const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
+    const int row = p.row_begin + r;
+    const int h = hg * p.hpw * kGqa + j;
+    raw* o;
+    if (RM == kRowVarlen) {
+        o = reinterpret_cast<raw*>(p.out) + ((long long)row * p.Hq + h) * kHeadDim + d0;
+    } else {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim + d0;
+    }
+    float acc[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) acc[e] = 0.0f;
+    float mx = -DV_INF;
+    const int lse_off = p.hpw * kGqa * kHeadDim + j;
+    for (int k = 0; k < cnt; ++k) mx = fmaxf(mx, p.part[(long long)(base + k) * p.slot_floats + lse_off]);
+    if (cnt > 0 && mx != -DV_INF) {
+        float wsum = 0.0f;
+        for (int k = 0; k < cnt; ++k) {
+            const float* sp = p.part + (long long)(base + k) * p.slot_floats;
+            const float lse = sp[lse_off];
+            if (lse == -DV_INF) continue;
+            const float wgt = exp2f(lse - mx);
+            wsum += wgt;
+            const float* src = sp + j * kHeadDim + d0;
+#pragma unroll
+            for (int e = 0; e < 32; e += 4) {
+                const f32x4 v = ld16f(src + e);
+                acc[e] += wgt * v[0];
+                acc[e + 1] += wgt * v[1];
+                acc[e + 2] += wgt * v[2];
+                acc[e + 3] += wgt * v[3];
+            }
+        }
+        const float inv = 1.0f / wsum;
+#pragma unroll
+        for (int e = 0; e < 32; ++e) acc[e] *= inv;
+    }
+    if constexpr (DT == kF32) {
+#pragma unroll
+        for (int e = 0; e < 32; e += 4) *reinterpret_cast<f32x4*>(o + e) = f32x4{acc[e], acc[e + 1], acc[e + 2], acc[e + 3]};
+    } else {
+#pragma unroll
+        for (int e = 0; e < 32; e += 8) {
+            const u32x4 pk = {pack2<DT>(acc[e], acc[e + 1]), pack2<DT>(acc[e + 2], acc[e + 3]),
+                              pack2<DT>(acc[e + 4], acc[e + 5]), pack2<DT>(acc[e + 6], acc[e + 7])};
+            *reinterpret_cast<u32x4*>(o + e) = pk;
+        }
+    }
+}
+
+// ---- host side --------------------------------------------------------------------
+
+namespace {
+
+struct DevInfo {
+    int cus = 0;
+    bool init = false;
+};
+
+DevInfo g_dev[64];
+
+int device_cus(int device) {
+    if (device < 0 || device >= 64) return 256;
+    DevInfo& d = g_dev[device];
+    if (!d.init) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c <= 0) c = 256;
+        d.cus = c;
+        d.init = true;
+    }
+    return d.cus;
+}
+
+int pick_hpw(int Hkv) {
+    if (Hkv % 4 == 0) return 4;
+    if (Hkv % 2 == 0) return 2;
+    return 1;
+}
+
+// workgroups per CU such that about eight waves share a CU
+int wgs_per_cu(int hpw) { return 8 / hpw; }
+
+// Resident workgroups per CU for one kernel instance at a given dynamic LDS
+// size, cached per 1 KiB of LDS (hipOccupancy queries cost host time).
+template <int DT, int QM, int KVM, int RM>
+int resident_wgs(int hpw, size_t lds) {
+    static int cache[4][161];  // [hpw-1][lds KiB]; 0 = not queried yet
+    const int kib = (int)((lds + 1023) / 1024);
+    if (kib > 160 || hpw < 1 || hpw > 4) return 1;
+    int& slot = cache[hpw - 1][kib];
+    if (slot == 0) {
+        int nb = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(&dv_decode<DT, QM, KVM, RM>),
+                                                         hpw * kWave, (size_t)kib * 1024) != hipSuccess ||
+            nb < 1)
+            nb = 1;
+        slot = nb;
+    }
+    return slot;
+}
+
+template <int DT, int QM, int KVM, int RM>
+hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, hipStream_t stream) {
+    const size_t lds = (size_t)p.hpw * vt_bytes<DT>() + (size_t)(p.nrows + 1) * sizeof(long long);
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_decode<DT, QM, KVM, RM>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    // one wave of workgroups that are all resident at once, bounded by the work
+    long long nwg = (long long)cus * resident_wgs<DT, QM, KVM, RM>(p.hpw, lds);
+    if (nwg > max_wg) nwg = max_wg;
+    if (nwg > cap) nwg = cap;
+    p.nwg = nwg < 1 ? 1 : (int)nwg;
+    hipLaunchKernelGGL((dv_decode<DT, QM, KVM, RM>), dim3(p.nwg), dim3(p.hpw * kWave), lds, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int nseg = p.nrows * (p.Hkv / p.hpw);
+    hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+template <int DT>
+hipError_t dispatch_modes(int qmode, int kvmode, int rowmode, const DecodeParams& p, long long max_wg,
+                          long long cap, int cus, hipStream_t stream) {
+    if (kvmode == kKvPaged && qmode == kQRotFull && rowmode == kRowWS)
+        return launch_one<DT, kQRotFull, kKvPaged, kRowWS>(p, max_wg, cap, cus, stream);
+    if (kvmode == kKvPaged && qmode == kQRotHalf && rowmode == kRowVarlen)
+        return launch_one<DT, kQRotHalf, kKvPaged, kRowVarlen>(p, max_wg, cap, cus, stream);
+    if (kvmode == kKvContig && qmode == kQPre && rowmode == kRowWS)
+        return launch_one<DT, kQPre, kKvContig, kRowWS>(p, max_wg, cap, cus, stream);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+size_t decode_workspace_bytes(int nrows_total, int Hkv, int device, int dtype) {
+    (void)dtype;
+    if (nrows_total <= 0 || Hkv <= 0) return 0;
+    const int hpw = pick_hpw(Hkv);
+    const int nhg = Hkv / hpw;
+    const int rows = nrows_total < kMaxRows ? nrows_total : kMaxRows;
+    const long long nwg = (long long)device_cus(device) * wgs_per_cu(hpw);
+    const long long nseg = (long long)rows * nhg;
+    const long long slot_floats = (long long)hpw * kGqa * (kHeadDim + 1);
+    const long long slots = nwg + nseg;
+    size_t bytes = (size_t)(slots * slot_floats * 4);
+    bytes = (bytes + 255) & ~(size_t)255;
+    bytes += (size_t)(nseg * 2 * 4);
+    return bytes;
+}
+
+hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const DecodeParams& base,
+                         int nrows_total, long long max_keys_per_row, void* workspace, size_t ws_bytes,
+                         hipStream_t stream) {
+    if (nrows_total <= 0 || base.Hkv <= 0) return hipSuccess;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    DecodeParams p = base;
+    p.hpw = pick_hpw(p.Hkv);
+    const int nhg = p.Hkv / p.hpw;
+    p.slot_floats = p.hpw * kGqa * (kHeadDim + 1);
+    const int cus = device_cus(device);
+    const long long max_wg = (long long)cus * wgs_per_cu(p.hpw);
+    const int rows_cap = nrows_total < kMaxRows ? nrows_total : kMaxRows;
+    const long long slots_cap = max_wg + (long long)rows_cap * nhg;
+    size_t part_bytes = (size_t)(slots_cap * p.slot_floats * 4);
+    part_bytes = (part_bytes + 255) & ~(size_t)255;
+    if (ws_bytes < part_bytes + (size_t)rows_cap * nhg * 2 * 4) return hipErrorInvalidValue;
+    p.part = reinterpret_cast<float*>(workspace);
+    p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
+    for (int r0 = 0; r0 < nrows_total; r0 += kMaxRows) {
+        p.row_begin = r0;
+        p.nrows = nrows_total - r0 < kMaxRows ? nrows_total - r0 : kMaxRows;
+        // enough workgroups to fill the chip, never more than the key count allows
+        const long long cap = ((long long)p.nrows * nhg * max_keys_per_row + p.min_keys - 1) / p.min_keys;
+        switch (dtype) {
+            case kBF16: e = dispatch_modes<kBF16>(qmode, kvmode, rowmode, p, max_wg, cap, cus, stream); break;
+            case kF16: e = dispatch_modes<kF16>(qmode, kvmode, rowmode, p, max_wg, cap, cus, stream); break;
+            case kF32: e = dispatch_modes<kF32>(qmode, kvmode, rowmode, p, max_wg, cap, cus, stream); break;
+            default: e = hipErrorInvalidValue;
+        }
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace dv

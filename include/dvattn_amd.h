@@ -1,0 +1,168 @@
+/*
+ * dvattn_amd.h -- C ABI of the MI355X (gfx950) DVAttn library, libdvattn_amd.so.
+ *
+ * Drop-in replacement for the compute entry points behind the reference's
+ * `libdvatt` torch operators.  Every function here is plain C: raw device
+ * pointers, int sizes, a caller-owned device workspace and a HIP stream passed
+ * as `void*`.  Nothing throws across this boundary; each call returns a
+ * dvattn_status and, on failure, leaves a message for dvattn_last_error().
+ *
+ * Reference interfaces replaced (paths in the reference repository):
+ *   dvattn_paged_sdpa        <- op `dvattn_paged_sdpa`, src/binding.cu:412-413,151-203
+ *                               (+ rope_gpu src/rope.cuh:54-65 and
+ *                               paged_v21::dvattn_paged_attention_gpu
+ *                               src/kernels/paged_kernel_v21.cuh:377-431)
+ *   dvattn_varlen_paged_sdpa <- op `dvattn_varlen_paged_sdpa`, src/binding.cu:418-420,249-296
+ *                               (+ rope_varlen_gpu src/rope.cuh:102-114 and
+ *                               src/kernels/varlen_paged_kernel_v21.cuh:373-428)
+ *   dvattn_sdpa              <- op `dvattn_sdpa`, src/binding.cu:410-411,79-149
+ *                               (+ v21::dvattn_attention_gpu src/kernels/kernel_v21.cuh:369-414)
+ *   dvattn_fused             <- op `dvattn_fused`, src/binding.cu:415-416,356-372
+ *   dvattn_rope              <- op `dvattn_rope`, src/binding.cu:414,41-77 (rope_gpu)
+ *   dvattn_varlen_rope       <- op `dvattn_varlen_rope`, src/binding.cu:417,205-247
+ *   dvattn_shape             <- struct Shape, src/common.h:5-20
+ *
+ * Semantics (identical to the reference operators):
+ *   - GQA factor 16 (Hq == 16*Hkv) and head dims E == Ev == 128 only; other
+ *     shapes are rejected with DVATTN_ERR_UNSUPPORTED (the reference printed a
+ *     message and returned/no-op'd, paged_kernel_v21.cuh:426-429, kernel_v21.cuh:410-413).
+ *   - Query rotation: dims e < R use x*cos - rotate_half(x)*sin with the first
+ *     R/2 entries of each cos/sin row (full width [.., R] for paged/contiguous,
+ *     half width [.., R/2] for varlen); dims >= R are copied.  fp32 math,
+ *     rotated query rounded to the storage type before the dot products.
+ *   - Key l of view f is visible to a query iff 0 <= l <= locations[f, row]
+ *     and l < fragment_lengths[f]; one softmax over all visible keys of all
+ *     views; fp32 accumulation; a query row with no visible key outputs zeros.
+ *   - Paged views are laid out back to back in each sequence's logical token
+ *     stream: view f starts at sum_{g<f} fragment_lengths[g]; logical position
+ *     p lives in page block_tables[w, p / block_size], row p % block_size of a
+ *     [num_blocks, block_size, Hkv, E] cache.
+ *   - Keys whose logical page is beyond the block_tables row, or whose page id
+ *     is outside [0, num_blocks), are treated as not visible (the reference
+ *     reads out of bounds there).
+ */
+#ifndef DVATTN_AMD_H
+#define DVATTN_AMD_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DVATTN_ABI_VERSION 1
+
+#if defined(__GNUC__) || defined(__clang__)
+#define DVATTN_API __attribute__((visibility("default")))
+#else
+#define DVATTN_API
+#endif
+
+/* Storage type of queries / keys / values / outputs (cos/sin are always fp32,
+ * index tensors int32), binding.cu:14-38. */
+typedef enum dvattn_dtype {
+    DVATTN_F32 = 0,
+    DVATTN_F16 = 1,
+    DVATTN_BF16 = 2
+} dvattn_dtype;
+
+typedef enum dvattn_status {
+    DVATTN_OK = 0,
+    DVATTN_ERR_INVALID = 1,     /* bad argument (null pointer, inconsistent sizes) */
+    DVATTN_ERR_UNSUPPORTED = 2, /* shape/dtype outside what the kernels implement */
+    DVATTN_ERR_WORKSPACE = 3,   /* workspace smaller than the *_workspace_size query */
+    DVATTN_ERR_HIP = 4          /* a HIP runtime call failed */
+} dvattn_status;
+
+/* Launch descriptor, mirrors Shape (src/common.h:5-20).  Fields an entry point
+ * does not use are ignored. */
+typedef struct dvattn_shape {
+    int F;                  /* views ("fragments") */
+    int W;                  /* sequences ("workers") */
+    int Hq;                 /* query heads (16 * Hkv) */
+    int Hkv;                /* key/value heads */
+    int E;                  /* q/k head dim (128) */
+    int Ev;                 /* v head dim (128) */
+    int S;                  /* query tokens per sequence (paged / contiguous) */
+    int block_size;         /* page size in tokens (paged, varlen) */
+    int max_blocks_per_seq; /* block_tables row length (paged, varlen) */
+    int total_q_tokens;     /* T (varlen) */
+    int num_blocks;         /* pages in k_cache / v_cache (paged, varlen) */
+    int rotary_dim;         /* R (even, <= E; 0 = no rotation) */
+} dvattn_shape;
+
+/* Last error message of the calling thread ("" if none). */
+DVATTN_API const char* dvattn_last_error(void);
+DVATTN_API int dvattn_abi_version(void);
+
+/* ---- paged decode attention with fused query RoPE --------------------------
+ * out [W,Hq,S,Ev] T; locations [F,W,S] i32; queries [W,Hq,S,E] T;
+ * cosines/sines [F,W,S,R] f32; fragment_lengths [F] i32 (device);
+ * k_cache [num_blocks,block_size,Hkv,E] T; v_cache [num_blocks,block_size,Hkv,Ev] T;
+ * block_tables [W,max_blocks_per_seq] i32.  All contiguous, on one device.
+ * Replaces binding.cu:151-203 / paged_kernel_v21.cuh:377-431. */
+DVATTN_API size_t dvattn_paged_sdpa_workspace_size(int dtype, const dvattn_shape* shape, int device);
+DVATTN_API dvattn_status dvattn_paged_sdpa(int dtype, void* out, float scale, const int* locations,
+                                const void* queries, const float* cosines, const float* sines,
+                                const int* fragment_lengths, const void* k_cache, const void* v_cache,
+                                const int* block_tables, const dvattn_shape* shape,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- varlen paged decode attention with fused query RoPE -------------------
+ * out [T,Hq,Ev] T; locations [F,T] i32 (a view with locations < 0 is skipped);
+ * queries [T,Hq,E] T; cosines/sines [F,T,R/2] f32 (half width);
+ * cu_seqlens_q [W+1] i32: token t belongs to the first sequence i with
+ * t < cu_seqlens_q[i+1] (sequence 0 if none); cu_seqlens_k is accepted and,
+ * as in the reference (binding.cu:279,290), not read.
+ * Replaces binding.cu:249-296 / varlen_paged_kernel_v21.cuh:373-428. */
+DVATTN_API size_t dvattn_varlen_paged_sdpa_workspace_size(int dtype, const dvattn_shape* shape, int device);
+DVATTN_API dvattn_status dvattn_varlen_paged_sdpa(int dtype, void* out, float scale, const int* locations,
+                                       const void* queries, const float* cosines, const float* sines,
+                                       const int* fragment_lengths, const void* k_cache,
+                                       const void* v_cache, const int* block_tables,
+                                       const int* cu_seqlens_q, const int* cu_seqlens_k,
+                                       const dvattn_shape* shape, void* workspace,
+                                       size_t workspace_bytes, void* stream);
+
+/* ---- contiguous-view attention on already-rotated queries ------------------
+ * out [W,Hq,S,Ev] T; locations [F,W,S]; rotated_queries [F,W,Hq,S,E] T;
+ * fragment_lengths [F] i32 (device).  key_fragments[f] / value_fragments[f]
+ * (host arrays of F device pointers) point at [B_f,Hkv,L_f,E|Ev] T tensors;
+ * fragment_tokens[f] = L_f and fragment_batch[f] = B_f (host arrays).  B_f is
+ * W, or 1 for a fragment shared by every sequence (the PyTorch reference
+ * broadcasts it, attention.py:45,53).  Visible keys are also bounded by L_f.
+ * Replaces binding.cu:79-149 / kernel_v21.cuh:369-414. */
+DVATTN_API size_t dvattn_sdpa_workspace_size(int dtype, const dvattn_shape* shape, int device);
+DVATTN_API dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* locations,
+                          const void* rotated_queries, const int* fragment_lengths,
+                          const void* const* key_fragments, const void* const* value_fragments,
+                          const int* fragment_tokens, const int* fragment_batch,
+                          const dvattn_shape* shape, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
+/* ---- rope + contiguous attention (dvattn_fused) -----------------------------
+ * Writes rotated_queries [F,W,Hq,S,E] (from queries [W,Hq,S,E] and full-width
+ * cos/sin [F,W,S,R]) and then runs dvattn_sdpa on it.
+ * Replaces binding.cu:356-372.  Same workspace size as dvattn_sdpa. */
+DVATTN_API dvattn_status dvattn_fused(int dtype, void* out, void* rotated_queries, float scale,
+                           const int* locations, const void* queries, const int* fragment_lengths,
+                           const void* const* key_fragments, const void* const* value_fragments,
+                           const int* fragment_tokens, const int* fragment_batch,
+                           const float* cosines, const float* sines, const dvattn_shape* shape,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- standalone query rotation ---------------------------------------------
+ * dvattn_rope: out [F,W,Hq,S,E] from queries [W,Hq,S,E], cos/sin [F,W,S,R].
+ * Replaces binding.cu:41-77 + rope.cuh:54-65.
+ * dvattn_varlen_rope: out [F,T,Hq,E] from queries [T,Hq,E], cos/sin [F,T,R/2].
+ * Replaces binding.cu:205-247 + rope.cuh:102-114. */
+DVATTN_API dvattn_status dvattn_rope(int dtype, void* out, const void* queries, const float* cosines,
+                          const float* sines, const dvattn_shape* shape, void* stream);
+DVATTN_API dvattn_status dvattn_varlen_rope(int dtype, void* out, const void* queries, const float* cosines,
+                                 const float* sines, const dvattn_shape* shape, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DVATTN_AMD_H */

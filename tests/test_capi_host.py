@@ -1,0 +1,162 @@
+"""Host-side tests of the native boundary (CPU only, no kernel launches).
+
+* libdvattn_amd.so loads and exports every function include/dvattn_amd.h declares.
+* Argument validation of the C ABI rejects bad calls before touching the GPU.
+* torch.ops.libdvatt carries the reference's six schemas (src/binding.cu:410-420)
+  with the needs_fixed_stride_order tag, and has no CPU kernels (no fallback).
+"""
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "dvattn_amd.h")
+
+REFERENCE_SCHEMAS = {
+    "dvattn_sdpa": "dvattn_sdpa(Tensor(a!) output, float scale, Tensor locations, Tensor queries, "
+                   "Tensor fragment_lengths, Tensor[] key_fragments, Tensor[] value_fragments) -> ()",
+    "dvattn_paged_sdpa": "dvattn_paged_sdpa(Tensor(a!) output, float scale, Tensor locations, Tensor queries, "
+                         "Tensor cosines, Tensor sines, Tensor fragment_lengths, Tensor k_cache, Tensor v_cache, "
+                         "Tensor block_tables) -> ()",
+    "dvattn_rope": "dvattn_rope(Tensor(a!) output, Tensor queries, Tensor cosines, Tensor sines) -> ()",
+    "dvattn_fused": "dvattn_fused(Tensor(a!) output, Tensor(b!) rq, float scale, Tensor locations, Tensor queries, "
+                    "Tensor fragment_lengths, Tensor[] key_fragments, Tensor[] value_fragments, Tensor cosines, "
+                    "Tensor sines) -> ()",
+    "dvattn_varlen_rope": "dvattn_varlen_rope(Tensor(a!) output, Tensor queries, Tensor cosines, Tensor sines) -> ()",
+    "dvattn_varlen_paged_sdpa": "dvattn_varlen_paged_sdpa(Tensor(a!) output, float scale, Tensor locations, "
+                                "Tensor queries, Tensor cosines, Tensor sines, Tensor fragment_lengths, "
+                                "Tensor k_cache, Tensor v_cache, Tensor block_tables, Tensor cu_seqlens_q, "
+                                "Tensor cu_seqlens_k) -> ()",
+}
+
+
+def header_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"DVATTN_API\s+[\w\s\*]*?\b(dvattn_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    from dvattention_amd import capi
+    assert header_functions() == sorted(capi.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    from dvattention_amd import capi
+    lib = capi.lib()
+    for name in header_functions():
+        assert hasattr(lib, name), f"{name} declared in include/dvattn_amd.h but not exported"
+    assert lib.dvattn_abi_version() == 1
+
+
+def _shape(**kw):
+    from dvattention_amd import capi
+    base = dict(F=1, W=1, Hq=16, Hkv=1, E=128, Ev=128, S=1, block_size=16, max_blocks_per_seq=4,
+                total_q_tokens=1, num_blocks=4, rotary_dim=64)
+    base.update(kw)
+    return capi.Shape(**base)
+
+
+def _paged(shape, dtype=2, out=1, ws_bytes=1 << 30):
+    from dvattention_amd import capi
+    L = capi.lib()
+    p = ctypes.c_void_p(0x1000)
+    return L.dvattn_paged_sdpa(dtype, p if out else None, 0.1, p, p, p, p, p, p, p, p, ctypes.byref(shape), p,
+                               ws_bytes, None)
+
+
+@pytest.mark.parametrize("kw,status,needle", [
+    (dict(Hq=32), 2, "GQA 16"),
+    (dict(E=64), 2, "E == Ev == 128"),
+    (dict(Ev=64), 2, "E == Ev == 128"),
+    (dict(rotary_dim=63), 2, "rotary_dim"),
+    (dict(rotary_dim=130), 2, "rotary_dim"),
+    (dict(block_size=0), 1, "block_size"),
+    (dict(F=-1), 1, "negative"),
+])
+def test_paged_rejects_unsupported_shapes(kw, status, needle):
+    from dvattention_amd import capi
+    st = _paged(_shape(**kw))
+    assert st == status
+    assert needle in capi.lib().dvattn_last_error().decode()
+
+
+def test_paged_rejects_bad_dtype_and_null_output_and_small_workspace():
+    from dvattention_amd import capi
+    L = capi.lib()
+    assert _paged(_shape(), dtype=7) == 2
+    assert "dtype" in L.dvattn_last_error().decode()
+    assert _paged(_shape(), out=0) == 1
+    assert _paged(_shape(), ws_bytes=16) == 3
+    assert "workspace" in L.dvattn_last_error().decode()
+
+
+def test_empty_problems_succeed_without_launch():
+    # W*S == 0 -> nothing to do (paged_kernel_v21.cuh:385-386)
+    assert _paged(_shape(W=0)) == 0
+    assert _paged(_shape(S=0)) == 0
+
+
+def test_rope_validation():
+    from dvattention_amd import capi
+    L = capi.lib()
+    p = ctypes.c_void_p(0x1000)
+    s = _shape(rotary_dim=7)
+    assert L.dvattn_rope(2, p, p, p, p, ctypes.byref(s), None) == 2
+    s = _shape(F=0)
+    assert L.dvattn_rope(2, p, p, p, p, ctypes.byref(s), None) == 0      # empty -> no-op (rope.cuh:58-60)
+
+
+def test_contig_rejects_bad_fragment_batch():
+    from dvattention_amd import capi
+    L = capi.lib()
+    p = ctypes.c_void_p(0x1000)
+    s = _shape(W=3, F=1)
+    kp = (ctypes.c_void_p * 1)(0x2000)
+    toks = (ctypes.c_int * 1)(8)
+    batch = (ctypes.c_int * 1)(2)              # neither 1 nor W
+    st = L.dvattn_sdpa(2, p, 0.1, p, p, p, kp, kp, toks, batch, ctypes.byref(s), p, 1 << 30, None)
+    assert st == 1 and "batch" in L.dvattn_last_error().decode()
+
+
+def test_workspace_query_is_bounded():
+    from dvattention_amd import capi
+    L = capi.lib()
+    s = _shape(W=32, Hkv=8, Hq=128)
+    n = L.dvattn_paged_sdpa_workspace_size(2, ctypes.byref(s), 0)
+    assert 0 < n < 64 << 20
+
+
+def test_torch_ops_schemas_match_reference():
+    import dvattention_amd  # noqa: F401  (registers torch.ops.libdvatt)
+    for name, schema in REFERENCE_SCHEMAS.items():
+        op = getattr(torch.ops.libdvatt, name).default
+        assert str(op._schema) == "libdvatt::" + schema
+        assert torch.Tag.needs_fixed_stride_order in op.tags
+
+
+def test_no_cpu_fallback():
+    import dvattention_amd
+    q = torch.zeros(1, 16, 1, 128)
+    c = torch.zeros(1, 1, 1, 64)
+    with pytest.raises(Exception):
+        dvattention_amd.dvattn_rope(q, c, c)
+
+
+def test_python_api_mirrors_reference_names():
+    import inspect
+    import dvattention_amd.attention as A
+    sig = inspect.signature(A.dvattn_fused)
+    assert list(sig.parameters)[:8] == ["queries", "locations", "keys", "values", "scale", "fragment_lengths",
+                                        "cosines", "sines"]
+    assert sig.parameters["rotated_queries"].kind is inspect.Parameter.KEYWORD_ONLY
+    assert list(inspect.signature(A.dvattn_sdpa).parameters) == ["queries", "locations", "keys", "values", "scale",
+                                                                 "fragment_lengths", "out"]
+    assert list(inspect.signature(A.dvattn_rope).parameters) == ["queries", "cosines", "sines", "out"]
+    x = torch.randn(2, 3, 4, 8)
+    c = torch.randn(2, 4, 6)
+    s = torch.randn(2, 4, 6)
+    y = A.apply_rotary_pos_emb(x, c, s)
+    assert torch.equal(y[..., 6:], x[..., 6:])

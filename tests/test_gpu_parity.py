@@ -1,0 +1,341 @@
+"""GPU parity of the HIP kernels against the CPU oracle (marked ``gpu``).
+
+Tolerances (max-abs against the fp32 oracle): fp32 1e-5, fp16 1e-3, bf16 2e-2.
+The query rotation is compared bit-exactly; page-table / varlen indexing is
+checked bit-exactly through GPU-vs-GPU identities (page permutation, split
+invariance) and exact special cases.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import dvattn_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = {torch.float32: 1e-5, torch.float16: 1e-3, torch.bfloat16: 2e-2}
+DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+
+def hf_cs(pos, R, base=1e4):
+    pos = np.asarray(pos, dtype=np.float64)
+    inv = 1.0 / (base ** (np.arange(0, R, 2, dtype=np.float64) / R))
+    fr = pos[..., None] * inv
+    emb = np.concatenate([fr, fr], -1)
+    return torch.from_numpy(np.cos(emb).astype(np.float32)), torch.from_numpy(np.sin(emb).astype(np.float32))
+
+
+def close(gpu_out, ref, dtype, what=""):
+    err = (gpu_out.float().cpu() - ref.float()).abs().max().item() if ref.numel() else 0.0
+    assert err <= TOL[dtype], f"{what}: max-abs error {err} > {TOL[dtype]} ({dtype})"
+    return err
+
+
+@pytest.fixture(scope="module")
+def dv(gpu):
+    import dvattention_amd
+    return dvattention_amd
+
+
+def to(d, dev):
+    return {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in d.items()}
+
+
+# ------------------------------------------------------------------ rope ---
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("E,R", [(128, 128), (128, 64), (128, 32), (128, 8), (128, 0), (64, 24), (100, 20)])
+def test_rope_bit_exact(dv, gpu, dtype, E, R):
+    F, W, Hq, S = 3, 2, 4, 3
+    q = torch.randn(W, Hq, S, E).to(dtype)
+    c, s = hf_cs(np.random.default_rng(E + R).integers(0, 70000, size=(F, W, S)), R) if R else \
+        (torch.zeros(F, W, S, 0), torch.zeros(F, W, S, 0))
+    ref = O.rope_q(q, c, s)
+    out = dv.dvattn_rope(q.to(gpu), c.to(gpu), s.to(gpu))
+    assert torch.equal(out.cpu(), ref)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("R", [128, 64, 16, 0])
+def test_varlen_rope_bit_exact(dv, gpu, dtype, R):
+    F, T, H, E = 4, 5, 8, 128
+    q = torch.randn(T, H, E).to(dtype)
+    c, s = hf_cs(np.random.default_rng(R).integers(0, 65536, size=(F, T)), R)
+    c, s = c[..., : R // 2].contiguous(), s[..., : R // 2].contiguous()
+    ref = O.rope_q_varlen(q, c, s)
+    out = dv.dvattn_varlen_rope(q.to(gpu), c.to(gpu), s.to(gpu))
+    assert torch.equal(out.cpu(), ref)
+
+
+def test_rope_through_c_abi(gpu):
+    from dvattention_amd import capi
+    q = torch.randn(2, 32, 1, 128).to(torch.bfloat16)
+    c, s = hf_cs(np.array([[[5], [900]], [[77], [123]]]), 64)
+    out = torch.empty(2, 2, 32, 1, 128, dtype=torch.bfloat16, device=gpu)
+    capi.rope(out, q.to(gpu), c.to(gpu), s.to(gpu))
+    assert torch.equal(out.cpu(), O.rope_q(q, c, s))
+
+
+# ----------------------------------------------------------------- paged ---
+
+def rand_paged(F, W, S, Hkv, bs, lens, R, dtype, seed, extra_pages=3, loc=None, k_scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    Hq, E = 16 * Hkv, 128
+    lens = np.asarray(lens)
+    maxB = int((lens.sum() + bs - 1) // bs) + 1
+    P = W * maxB + extra_pages
+    bt = rng.permutation(P)[: W * maxB].astype(np.int32).reshape(W, maxB)
+    if loc is None:
+        loc = rng.integers(-2, lens.max() + 3, size=(F, W, S)).astype(np.int32)
+    c, s = hf_cs(rng.integers(0, 70000, size=(F, W, S)), R) if R else \
+        (torch.zeros(F, W, S, 0), torch.zeros(F, W, S, 0))
+    return dict(locations=torch.from_numpy(np.asarray(loc, dtype=np.int32)),
+                queries=torch.randn(W, Hq, S, E, generator=g).to(dtype), cosines=c, sines=s,
+                fragment_lengths=torch.from_numpy(lens.astype(np.int32)),
+                k_cache=(torch.randn(P, bs, Hkv, E, generator=g) * k_scale).to(dtype),
+                v_cache=torch.randn(P, bs, Hkv, E, generator=g).to(dtype),
+                block_tables=torch.from_numpy(bt))
+
+
+def run_paged(dv, d, scale, gpu):
+    g = to(d, gpu)
+    return dv.dvattn_paged_sdpa(g["queries"], g["locations"], g["cosines"], g["sines"], g["fragment_lengths"],
+                                g["k_cache"], g["v_cache"], g["block_tables"], scale)
+
+
+PAGED_CASES = [
+    # F, W, S, Hkv, bs, lens, R
+    (1, 1, 1, 1, 16, [512], 64),
+    (1, 3, 1, 8, 16, [700], 128),
+    (2, 2, 1, 4, 16, [33, 100], 128),
+    (3, 2, 3, 2, 5, [40, 0, 77], 32),
+    (1, 2, 2, 1, 64, [300], 0),
+    (2, 1, 4, 2, 1, [20, 9], 16),
+    (4, 2, 1, 3, 8, [15, 64, 1, 40], 64),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", PAGED_CASES)
+def test_paged_vs_oracle(dv, gpu, dtype, case):
+    F, W, S, Hkv, bs, lens, R = case
+    d = rand_paged(F, W, S, Hkv, bs, lens, R, dtype, seed=hash((F, W, S, Hkv, bs, R)) & 0xffff)
+    scale = 128 ** -0.5
+    out = run_paged(dv, d, scale, gpu)
+    ref = O.paged_sdpa(scale, **d)
+    close(out, ref, dtype, f"paged {case}")
+
+
+def test_paged_through_c_abi_matches_torch_op(dv, gpu):
+    from dvattention_amd import capi
+    d = rand_paged(2, 4, 1, 8, 16, [300, 220], 128, torch.bfloat16, seed=3)
+    g = to(d, gpu)
+    a = run_paged(dv, d, 0.1, gpu)
+    b = torch.empty_like(a)
+    capi.paged_sdpa(b, 0.1, g["locations"], g["queries"], g["cosines"], g["sines"], g["fragment_lengths"],
+                    g["k_cache"], g["v_cache"], g["block_tables"])
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    close(b, O.paged_sdpa(0.1, **d), torch.bfloat16)
+
+
+def test_paged_page_permutation_bit_exact(dv, gpu):
+    d = rand_paged(2, 3, 1, 8, 16, [257, 130], 128, torch.bfloat16, seed=8, extra_pages=0)
+    a = run_paged(dv, d, 0.09, gpu)
+    P = d["k_cache"].shape[0]
+    perm = torch.from_numpy(np.random.default_rng(2).permutation(P))
+    inv = torch.argsort(perm)
+    d2 = dict(d, k_cache=d["k_cache"][perm], v_cache=d["v_cache"][perm],
+              block_tables=inv[d["block_tables"].long()].to(torch.int32))
+    b = run_paged(dv, d2, 0.09, gpu)
+    assert torch.equal(a, b)
+
+
+def test_paged_single_visible_key_exact(dv, gpu):
+    for dtype in DTYPES:
+        d = rand_paged(2, 3, 1, 2, 16, [40, 30], 64, dtype, seed=4)
+        d["locations"][0] = -1
+        d["locations"][1] = 0
+        out = run_paged(dv, d, 0.3, gpu).cpu()
+        for w in range(3):
+            p = 40
+            page = int(d["block_tables"][w, p // 16])
+            for h in range(32):
+                assert torch.equal(out[w, h, 0], d["v_cache"][page, p % 16, h // 16]), (dtype, w, h)
+
+
+def test_paged_empty_rows_zero_and_noop(dv, gpu):
+    d = rand_paged(2, 3, 2, 1, 16, [50, 20], 64, torch.float16, seed=5)
+    d["locations"][:, 1] = -3
+    out = run_paged(dv, d, 0.2, gpu).cpu()
+    assert torch.count_nonzero(out[1]) == 0
+    assert torch.count_nonzero(out[0]) > 0
+    # no query rows: output untouched (paged_kernel_v21.cuh:385-386)
+    g = to(rand_paged(1, 2, 1, 1, 16, [10], 64, torch.float16, seed=6), gpu)
+    empty = torch.full((0, 16, 1, 128), 7.0, dtype=torch.float16, device=gpu)
+    torch.ops.libdvatt.dvattn_paged_sdpa(empty, 0.1, g["locations"][:, :0], g["queries"][:0], g["cosines"][:, :0],
+                                         g["sines"][:, :0], g["fragment_lengths"], g["k_cache"], g["v_cache"],
+                                         g["block_tables"])
+
+
+def test_paged_invalid_pages_are_masked(dv, gpu):
+    # a block_tables entry outside the page pool hides its keys (no out-of-bounds read)
+    d = rand_paged(1, 2, 1, 1, 16, [64], 64, torch.float32, seed=7, loc=np.array([[[63], [63]]]))
+    bt = d["block_tables"].clone()
+    bt[0, 1] = 10 ** 6                      # keys 16..31 of sequence 0
+    out = run_paged(dv, dict(d, block_tables=bt), 0.1, gpu).cpu()
+    full = O.paged_sdpa(0.1, **d)
+    close(out[1], full[1], torch.float32, "untouched sequence")
+    rq = O.rope_q(d["queries"], d["cosines"], d["sines"])[0, 0]         # [Hq,1,E]
+    pos = np.array(list(range(16)) + list(range(32, 64)))
+    pages = d["block_tables"][0].numpy()[pos // 16]
+    k = d["k_cache"][pages, pos % 16, 0]                               # [n,E]
+    v = d["v_cache"][pages, pos % 16, 0]
+    ref0 = torch.softmax(0.1 * (rq[:, 0] @ k.T), -1) @ v
+    close(out[0, :, 0], ref0, torch.float32, "sequence with a hole")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_paged_non_default_stream_and_determinism(dv, gpu, dtype):
+    d = rand_paged(1, 4, 1, 8, 16, [900], 128, dtype, seed=11)
+    a = run_paged(dv, d, 0.1, gpu)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        b = run_paged(dv, d, 0.1, gpu)
+    s.synchronize()
+    assert torch.equal(a, b)
+
+
+# ---------------------------------------------------------------- varlen ---
+
+def rand_varlen(F, W, T, cu_q, Hkv, bs, lens, R, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens)
+    maxB = int((lens.sum() + bs - 1) // bs) + 1
+    P = W * maxB
+    bt = rng.permutation(P).astype(np.int32).reshape(W, maxB)
+    loc = rng.integers(-3, lens.max() + 2, size=(F, T)).astype(np.int32)
+    c, s = hf_cs(rng.integers(0, 65536, size=(F, T)), R)
+    c, s = c[..., : R // 2].contiguous(), s[..., : R // 2].contiguous()
+    return dict(locations=torch.from_numpy(loc), queries=torch.randn(T, 16 * Hkv, 128, generator=g).to(dtype),
+                cosines=c, sines=s, fragment_lengths=torch.from_numpy(lens.astype(np.int32)),
+                k_cache=torch.randn(P, bs, Hkv, 128, generator=g).to(dtype),
+                v_cache=torch.randn(P, bs, Hkv, 128, generator=g).to(dtype),
+                block_tables=torch.from_numpy(bt), cu_seqlens_q=torch.tensor(cu_q, dtype=torch.int32),
+                cu_seqlens_k=torch.zeros(W + 1, dtype=torch.int32))
+
+
+def run_varlen(dv, d, scale, gpu):
+    g = to(d, gpu)
+    return dv.dvattn_varlen_paged_sdpa(g["queries"], g["locations"], g["cosines"], g["sines"],
+                                       g["fragment_lengths"], g["k_cache"], g["v_cache"], g["block_tables"],
+                                       g["cu_seqlens_q"], g["cu_seqlens_k"], scale)
+
+
+VARLEN_CASES = [
+    # F, W, T, cu_q, Hkv, bs, lens, R
+    (4, 5, 5, [0, 1, 2, 3, 4, 5], 4, 16, [300, 120, 77, 500], 64),
+    (2, 3, 7, [0, 2, 2, 7], 1, 8, [40, 90], 128),
+    (3, 3, 6, [0, 4, 2, 5], 2, 16, [20, 6, 33], 32),      # malformed cu_seqlens_q
+    (1, 2, 3, [0, 1, 2], 1, 3, [50], 0),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", VARLEN_CASES)
+def test_varlen_vs_oracle(dv, gpu, dtype, case):
+    F, W, T, cu_q, Hkv, bs, lens, R = case
+    d = rand_varlen(F, W, T, cu_q, Hkv, bs, lens, R, dtype, seed=T * 7 + F)
+    out = run_varlen(dv, d, 0.088, gpu)
+    ref = O.varlen_paged_sdpa(0.088, **d)
+    close(out, ref, dtype, f"varlen {case}")
+
+
+def test_varlen_through_c_abi(dv, gpu):
+    from dvattention_amd import capi
+    d = rand_varlen(4, 5, 5, [0, 1, 2, 3, 4, 5], 4, 16, [300, 120, 77, 500], 64, torch.float16, seed=1)
+    g = to(d, gpu)
+    out = torch.empty(5, 64, 128, dtype=torch.float16, device=gpu)
+    capi.varlen_paged_sdpa(out, 0.1, g["locations"], g["queries"], g["cosines"], g["sines"], g["fragment_lengths"],
+                           g["k_cache"], g["v_cache"], g["block_tables"], g["cu_seqlens_q"], g["cu_seqlens_k"])
+    torch.cuda.synchronize()
+    close(out, O.varlen_paged_sdpa(0.1, **d), torch.float16)
+
+
+def test_varlen_many_rows_multi_launch(dv, gpu):
+    # more query rows than one launch's schedule holds (4096): exercises the row split
+    T = 5000
+    W = T
+    d = rand_varlen(1, W, T, list(range(T + 1)), 1, 16, [24], 64, torch.bfloat16, seed=9)
+    out = run_varlen(dv, d, 0.1, gpu).cpu()
+    ref = O.varlen_paged_sdpa(0.1, **d)
+    close(out, ref, torch.bfloat16, "varlen T=5000")
+
+
+# ------------------------------------------------------------ contiguous ---
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("F,W,S,Hkv,Ls,batch", [
+    (1, 1, 1, 1, [512], [1]),
+    (2, 3, 2, 2, [100, 37], [3, 1]),
+    (3, 2, 1, 1, [16, 0, 90], [0, 2, 2]),        # 0: 3-D fragment
+    (20, 2, 1, 1, [5 + 3 * i for i in range(20)], [2] * 20),   # F > 16: device fragment table
+])
+def test_sdpa_and_fused_vs_oracle(dv, gpu, dtype, F, W, S, Hkv, Ls, batch):
+    g = torch.Generator().manual_seed(F * 100 + W)
+    rng = np.random.default_rng(F)
+    keys, vals = [], []
+    for L, B in zip(Ls, batch):
+        shp = (Hkv, L, 128) if B == 0 else (B, Hkv, L, 128)
+        keys.append(torch.randn(shp, generator=g).to(dtype))
+        vals.append(torch.randn(shp, generator=g).to(dtype))
+    loc = torch.from_numpy(rng.integers(-1, max(Ls) + 2, size=(F, W, S)).astype(np.int32))
+    fl = torch.tensor(Ls, dtype=torch.int32)
+    q = torch.randn(W, 16 * Hkv, S, 128, generator=g).to(dtype)
+    c, s = hf_cs(rng.integers(0, 9000, size=(F, W, S)), 64)
+    rq_ref = O.rope_q(q, c, s)
+    ref = O.contig_sdpa(0.1, loc, rq_ref, fl, keys, vals)
+    gk = [k.to(gpu) for k in keys]
+    gv = [v.to(gpu) for v in vals]
+    out = dv.dvattn_sdpa(rq_ref.to(gpu), loc.to(gpu), gk, gv, 0.1, fl.to(gpu))
+    close(out, ref, dtype, "dvattn_sdpa")
+    rq = torch.empty(F, W, 16 * Hkv, S, 128, dtype=dtype, device=gpu)
+    out2 = torch.empty(W, 16 * Hkv, S, 128, dtype=dtype, device=gpu)
+    dv.dvattn_fused(q.to(gpu), loc.to(gpu), gk, gv, 0.1, fl.to(gpu), c.to(gpu), s.to(gpu), rotated_queries=rq,
+                    out=out2)
+    assert torch.equal(rq.cpu(), rq_ref)
+    assert torch.equal(out2, out)
+
+
+def test_fused_through_c_abi(gpu):
+    from dvattention_amd import capi
+    q = torch.randn(1, 16, 1, 128)
+    k = torch.randn(1, 1, 512, 128)
+    v = torch.randn(1, 1, 512, 128)
+    loc = torch.tensor([[[512]]], dtype=torch.int32)
+    fl = torch.tensor([512], dtype=torch.int32)
+    c, s = hf_cs(np.array([[[512]]]), 64)
+    out = torch.empty(1, 16, 1, 128, device=gpu)
+    rq = torch.empty(1, 1, 16, 1, 128, device=gpu)
+    capi.fused(out, rq, 128 ** -0.5, loc.to(gpu), q.to(gpu), fl.to(gpu), [k.to(gpu)], [v.to(gpu)], c.to(gpu),
+               s.to(gpu))
+    torch.cuda.synchronize()
+    ref, rq_ref = O.fused(128 ** -0.5, loc, q, fl, [k], [v], c, s)
+    assert torch.equal(rq.cpu(), rq_ref)
+    close(out, ref, torch.float32)
+
+
+def test_errors_raise(dv, gpu):
+    d = to(rand_paged(1, 1, 1, 1, 16, [10], 64, torch.float32, seed=1), gpu)
+    with pytest.raises(RuntimeError):       # int64 locations
+        dv.dvattn_paged_sdpa(d["queries"], d["locations"].long(), d["cosines"], d["sines"], d["fragment_lengths"],
+                             d["k_cache"], d["v_cache"], d["block_tables"], 0.1)
+    with pytest.raises(RuntimeError):       # GQA 8 unsupported
+        dv.dvattn_paged_sdpa(d["queries"][:, :8].contiguous(), d["locations"], d["cosines"], d["sines"],
+                             d["fragment_lengths"], d["k_cache"], d["v_cache"], d["block_tables"], 0.1)
+    with pytest.raises(RuntimeError):       # float64 unsupported
+        out = torch.empty(1, 16, 1, 128, dtype=torch.float64, device=gpu)
+        dv.dvattn_paged_sdpa(d["queries"].double(), d["locations"], d["cosines"], d["sines"], d["fragment_lengths"],
+                             d["k_cache"].double(), d["v_cache"].double(), d["block_tables"], 0.1, out=out)
