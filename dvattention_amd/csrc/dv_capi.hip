@@ -29,7 +29,7 @@ dvattn_status ok() {
 }
 
 dvattn_status hip_fail(hipError_t e, const char* what) {
-    return fail(DVATTN_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+    return fail(DVATTN_ERR_HIP, "%s: %s (%s)", what, hipGetErrorString(e), dv::last_hip_site());
 }
 
 bool valid_dtype(int dt) { return dt == DVATTN_F32 || dt == DVATTN_F16 || dt == DVATTN_BF16; }

@@ -91,5 +91,7 @@ hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const De
                          int nrows_total, long long max_keys_per_row, void* workspace, size_t ws_bytes,
                          hipStream_t stream);
 hipError_t launch_rope(int dtype, const RopeParams& p, hipStream_t stream);
+// Which runtime call produced the last error returned by launch_decode (this thread).
+const char* last_hip_site();
 
 }  // namespace dv

@@ -689,6 +689,13 @@ __global__ __launch_bounds__(256) void dv_merge(const DecodeParams p) {
 
 namespace {
 
+thread_local const char* g_site = "";
+
+hipError_t note_site(hipError_t e, const char* site) {
+    g_site = site;
+    return e;
+}
+
 struct DevInfo {
     int cus = 0;
     bool init = false;
@@ -741,9 +748,11 @@ hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, 
     const size_t lds = (size_t)p.hpw * vt_bytes<DT>() + (size_t)(p.nrows + 1) * sizeof(long long);
     static bool attr_set = false;
     if (!attr_set) {
+        // largest dynamic LDS any launch of this kernel asks for (4 waves, kMaxRows rows)
+        const size_t max_lds = (size_t)kMaxWavesPerWg * vt_bytes<DT>() + (size_t)(kMaxRows + 1) * sizeof(long long);
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_decode<DT, QM, KVM, RM>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-        if (e != hipSuccess) return e;
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
+        if (e != hipSuccess) return note_site(e, "hipFuncSetAttribute(dv_decode)");
         attr_set = true;
     }
     // one wave of workgroups that are all resident at once, bounded by the work
@@ -753,10 +762,12 @@ hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, 
     p.nwg = nwg < 1 ? 1 : (int)nwg;
     hipLaunchKernelGGL((dv_decode<DT, QM, KVM, RM>), dim3(p.nwg), dim3(p.hpw * kWave), lds, stream, p);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    if (e != hipSuccess) return note_site(e, "launch dv_decode");
     const int nseg = p.nrows * (p.Hkv / p.hpw);
     hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg), dim3(256), 0, stream, p);
-    return hipGetLastError();
+    e = hipGetLastError();
+    if (e != hipSuccess) return note_site(e, "launch dv_merge");
+    return hipSuccess;
 }
 
 template <int DT>
@@ -772,6 +783,8 @@ hipError_t dispatch_modes(int qmode, int kvmode, int rowmode, const DecodeParams
 }
 
 }  // namespace
+
+const char* last_hip_site() { return g_site; }
 
 size_t decode_workspace_bytes(int nrows_total, int Hkv, int device, int dtype) {
     (void)dtype;

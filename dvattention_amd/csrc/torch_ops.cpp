@@ -6,7 +6,7 @@
 // libdvattn_amd.so on the tensors' current HIP stream.  Unsupported dtypes and
 // shapes raise instead of silently doing nothing.
 #include <ATen/ATen.h>
-#include <c10/hip/HIPGuard.h>
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/library.h>
 
@@ -96,7 +96,7 @@ void dvattn_rope_op(at::Tensor& out, const at::Tensor& queries, const at::Tensor
     TORCH_CHECK(cosines.size(0) == F && cosines.size(1) == W && cosines.size(2) == S,
                 "dvattn_rope: cosines must be [F,W,S,R], got ", cosines.sizes());
     TORCH_CHECK(sines.sizes() == cosines.sizes(), "dvattn_rope: sines must match cosines, got ", sines.sizes());
-    c10::hip::HIPGuard guard(out.device());
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
     dvattn_shape s{};
     s.F = as_int(F, "F");
     s.W = as_int(W, "W");
@@ -135,7 +135,7 @@ void dvattn_varlen_rope_op(at::Tensor& out, const at::Tensor& queries, const at:
                 cosines.sizes());
     TORCH_CHECK(sines.sizes() == cosines.sizes(), "dvattn_varlen_rope: sines must match cosines, got ",
                 sines.sizes());
-    c10::hip::HIPGuard guard(out.device());
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
     dvattn_shape s{};
     s.F = as_int(F, "F");
     s.total_q_tokens = as_int(T, "T");
@@ -198,7 +198,7 @@ void dvattn_paged_sdpa_op(at::Tensor& out, double scale, const at::Tensor& locat
                 "dvattn_paged_sdpa: v_cache must be [num_blocks, block_size, Hkv, Ev], got ", v_cache.sizes());
     TORCH_CHECK(block_tables.size(0) >= W, "dvattn_paged_sdpa: block_tables needs a row per sequence (", W,
                 "), got ", block_tables.sizes());
-    c10::hip::HIPGuard guard(out.device());
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
     dvattn_shape s{};
     s.F = as_int(F, "F");
     s.W = as_int(W, "W");
@@ -274,7 +274,7 @@ void dvattn_varlen_paged_sdpa_op(at::Tensor& out, double scale, const at::Tensor
                 "dvattn_varlen_paged_sdpa: block_tables needs a row per sequence (", W, "), got ",
                 block_tables.sizes());
     TORCH_CHECK(W > 0 || T == 0, "dvattn_varlen_paged_sdpa: tokens without any sequence (cu_seqlens_q has 1 entry)");
-    c10::hip::HIPGuard guard(out.device());
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
     dvattn_shape s{};
     s.F = as_int(F, "F");
     s.W = as_int(W, "W");
@@ -362,7 +362,7 @@ void sdpa_common(at::Tensor& out, double scale, const at::Tensor& locations, con
         toks[f] = as_int(k.size(fo + 1), "fragment length");
         batch[f] = (int)B;
     }
-    c10::hip::HIPGuard guard(out.device());
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(out.device());
     dvattn_shape s{};
     s.F = as_int(F, "F");
     s.W = as_int(W, "W");
