@@ -136,7 +136,7 @@ dvattn_status dvattn_paged_sdpa(int dtype, void* out, float scale, const int* lo
     p.bs_shift = log2_exact(s->block_size);
     p.maxB = s->max_blocks_per_seq;
     p.nblocks = s->num_blocks;
-    p.min_keys = 128;
+    p.min_keys = 64;
     const long long max_keys = (long long)s->max_blocks_per_seq * s->block_size;
     hipError_t e = dv::launch_decode(dtype, dv::kQRotFull, dv::kKvPaged, dv::kRowWS, p, s->W * s->S, max_keys,
                                      workspace, workspace_bytes, (hipStream_t)stream);
@@ -199,7 +199,7 @@ dvattn_status dvattn_varlen_paged_sdpa(int dtype, void* out, float scale, const 
     p.bs_shift = log2_exact(s->block_size);
     p.maxB = s->max_blocks_per_seq;
     p.nblocks = s->num_blocks;
-    p.min_keys = 128;
+    p.min_keys = 64;
     const long long max_keys = (long long)s->max_blocks_per_seq * s->block_size;
     hipError_t e = dv::launch_decode(dtype, dv::kQRotHalf, dv::kKvPaged, dv::kRowVarlen, p, s->total_q_tokens,
                                      max_keys, workspace, workspace_bytes, (hipStream_t)stream);
@@ -282,7 +282,7 @@ dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* location
     p.R = 0;
     p.bs = 1;
     p.bs_shift = 0;
-    p.min_keys = 128;
+    p.min_keys = 64;
     hipError_t e = dv::launch_decode(dtype, dv::kQPre, dv::kKvContig, dv::kRowWS, p, s->W * s->S, max_keys, ws,
                                      ws_left, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa launch");

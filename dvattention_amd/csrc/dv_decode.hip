@@ -455,22 +455,13 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
             } else {
                 u32x4 qB[4];
                 load_q16<DT, QM, RM>(p, row, f, hkv, qB);
-                Kv16 b0, b1;
-                window_update<DT, KVM>(p, c, win, l0, l1);
-                issue16<DT, KVM>(p, c, win, b0, l0, l1);
-                for (int l = l0; l < l1; l += 2 * kStep) {
-                    const bool has1 = l + kStep < l1;
-                    if (has1) {
-                        window_update<DT, KVM>(p, c, win, l + kStep, l1);
-                        issue16<DT, KVM>(p, c, win, b1, l + kStep, l1);
-                    }
-                    compute16<DT>(st, b0, qB, vt, p.l2scale);
-                    if (!has1) break;
-                    if (l + 2 * kStep < l1) {
-                        window_update<DT, KVM>(p, c, win, l + 2 * kStep, l1);
-                        issue16<DT, KVM>(p, c, win, b0, l + 2 * kStep, l1);
-                    }
-                    compute16<DT>(st, b1, qB, vt, p.l2scale);
+                // One 32-key step in flight per wave; with two workgroups of four waves per
+                // CU, eight waves interleave their loads and MFMA work.
+                for (int l = l0; l < l1; l += kStep) {
+                    Kv16 b;
+                    window_update<DT, KVM>(p, c, win, l, l1);
+                    issue16<DT, KVM>(p, c, win, b, l, l1);
+                    compute16<DT>(st, b, qB, vt, p.l2scale);
                 }
             }
         }
@@ -620,68 +611,79 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
 
 // ---- split merge -------------------------------------------------------------------
 
-// One block per segment (row, head group).  count == 1: already final;
-// count == 0: no visible key -> zeros (paged_kernel_v21.cuh:318); otherwise the
-// LSE-weighted sum of the pieces (paged_kernel_v21.cuh:325-364).
+constexpr int kMergeBatch = 8;  // pieces whose loads are in flight together
+
+// Block (segment, KV head) with 256 threads: thread t handles query head t/16,
+// dims [(t%16)*8, +8).  count == 1: already final; count == 0: no visible key ->
+// zeros (paged_kernel_v21.cuh:318); otherwise the base-2-LSE-weighted sum of the
+// pieces' normalised outputs (paged_kernel_v21.cuh:325-364).
 template <int DT, int RM>
 __global__ __launch_bounds__(256) void dv_merge(const DecodeParams p) {
     using raw = typename Tr<DT>::raw;
-    const int sg = blockIdx.x;
-    const int NHG = p.Hkv / p.hpw;
+    const int sg = blockIdx.x / p.hpw;
+    const int wi = blockIdx.x - sg * p.hpw;
     const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
     if (cnt == 1) return;
+    const int NHG = p.Hkv / p.hpw;
     const int tid = threadIdx.x;
-    const int j = tid >> 2;  // head within the group
-    if (j >= p.hpw * kGqa) return;
-    const int d0 = (tid & 3) * 32;
+    const int n = tid >> 4;
+    const int d = (tid & 15) * 8;
     const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
     const int row = p.row_begin + r;
-    const int h = hg * p.hpw * kGqa + j;
+    const int h = (hg * p.hpw + wi) * kGqa + n;
     raw* o;
     if (RM == kRowVarlen) {
-        o = reinterpret_cast<raw*>(p.out) + ((long long)row * p.Hq + h) * kHeadDim + d0;
+        o = reinterpret_cast<raw*>(p.out) + ((long long)row * p.Hq + h) * kHeadDim + d;
     } else {
         const int w = row / p.S, s = row - (row / p.S) * p.S;
-        o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim + d0;
+        o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim + d;
     }
-    float acc[32];
-#pragma unroll
-    for (int e = 0; e < 32; ++e) acc[e] = 0.0f;
-    float mx = -DV_INF;
+    const int j = wi * kGqa + n;
     const int lse_off = p.hpw * kGqa * kHeadDim + j;
-    for (int k = 0; k < cnt; ++k) mx = fmaxf(mx, p.part[(long long)(base + k) * p.slot_floats + lse_off]);
-    if (cnt > 0 && mx != -DV_INF) {
-        float wsum = 0.0f;
-        for (int k = 0; k < cnt; ++k) {
-            const float* sp = p.part + (long long)(base + k) * p.slot_floats;
-            const float lse = sp[lse_off];
-            if (lse == -DV_INF) continue;
-            const float wgt = exp2f(lse - mx);
-            wsum += wgt;
-            const float* src = sp + j * kHeadDim + d0;
+    const int val_off = j * kHeadDim + d;
+    float m = -DV_INF, wsum = 0.0f;
+    float acc[8];
 #pragma unroll
-            for (int e = 0; e < 32; e += 4) {
-                const f32x4 v = ld16f(src + e);
-                acc[e] += wgt * v[0];
-                acc[e + 1] += wgt * v[1];
-                acc[e + 2] += wgt * v[2];
-                acc[e + 3] += wgt * v[3];
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    for (int k0 = 0; k0 < cnt; k0 += kMergeBatch) {
+        float lse[kMergeBatch];
+        f32x4 v0[kMergeBatch], v1[kMergeBatch];
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const bool in = k0 + i < cnt;
+            const float* sp = p.part + (long long)(base + (in ? k0 + i : k0)) * p.slot_floats;
+            lse[i] = in ? sp[lse_off] : -DV_INF;
+            v0[i] = ld16f(sp + val_off);
+            v1[i] = ld16f(sp + val_off + 4);
+        }
+        float bm = m;
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) bm = fmaxf(bm, lse[i]);
+        if (bm == -DV_INF) continue;
+        const float sc = exp2f(m - bm);  // m == -inf -> 0
+        wsum *= sc;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= sc;
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const float wgt = exp2f(lse[i] - bm);  // empty piece (-inf) -> 0
+            wsum += wgt;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[e] += wgt * v0[i][e];
+                acc[4 + e] += wgt * v1[i][e];
             }
         }
-        const float inv = 1.0f / wsum;
-#pragma unroll
-        for (int e = 0; e < 32; ++e) acc[e] *= inv;
+        m = bm;
     }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
     if constexpr (DT == kF32) {
-#pragma unroll
-        for (int e = 0; e < 32; e += 4) *reinterpret_cast<f32x4*>(o + e) = f32x4{acc[e], acc[e + 1], acc[e + 2], acc[e + 3]};
+        *reinterpret_cast<f32x4*>(o) = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
+        *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
     } else {
-#pragma unroll
-        for (int e = 0; e < 32; e += 8) {
-            const u32x4 pk = {pack2<DT>(acc[e], acc[e + 1]), pack2<DT>(acc[e + 2], acc[e + 3]),
-                              pack2<DT>(acc[e + 4], acc[e + 5]), pack2<DT>(acc[e + 6], acc[e + 7])};
-            *reinterpret_cast<u32x4*>(o + e) = pk;
-        }
+        const u32x4 pk = {pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv),
+                          pack2<DT>(acc[4] * inv, acc[5] * inv), pack2<DT>(acc[6] * inv, acc[7] * inv)};
+        *reinterpret_cast<u32x4*>(o) = pk;
     }
 }
 
@@ -764,7 +766,7 @@ hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return note_site(e, "launch dv_decode");
     const int nseg = p.nrows * (p.Hkv / p.hpw);
-    hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg * p.hpw), dim3(256), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return note_site(e, "launch dv_merge");
     return hipSuccess;

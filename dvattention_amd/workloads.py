@@ -138,7 +138,7 @@ def varlen_workload(name, *, W, Hkv, R, base, bs, dtype, device, seed, median=20
         for lp in touched[w]:
             bt[w, lp] = perm[o]
             o += 1
-    loc = np.where(np.arange(F)[None, :] < nv[:, None], lens - 1, -1).T.astype(np.int32)   # [F,T]
+    loc = np.ascontiguousarray(np.where(np.arange(F)[None, :] < nv[:, None], lens - 1, -1).T.astype(np.int32))  # [F,T]
     rel = rng.integers(0, max_offset + 1, size=(F, W))
     cos, sin = hf_cos_sin(rel, R, base)                     # [F,T,R]
     cos, sin = cos[..., : R // 2].contiguous(), sin[..., : R // 2].contiguous()
