@@ -90,6 +90,7 @@ int dvattn_abi_version(void) { return DVATTN_ABI_VERSION; }
 // ---------------------------------------------------------------------------
 size_t dvattn_paged_sdpa_workspace_size(int dtype, const dvattn_shape* s, int device) {
     if (!s || !valid_dtype(dtype)) return 0;
+    if (dv::use_chunk(dtype, s->S)) return dv::chunk_workspace_bytes(s->W, s->S, s->Hkv, current_device(device));
     return dv::decode_workspace_bytes(s->W * s->S, s->Hkv, current_device(device), dtype);
 }
 
@@ -138,8 +139,15 @@ dvattn_status dvattn_paged_sdpa(int dtype, void* out, float scale, const int* lo
     p.nblocks = s->num_blocks;
     p.min_keys = 64;
     const long long max_keys = (long long)s->max_blocks_per_seq * s->block_size;
-    hipError_t e = dv::launch_decode(dtype, dv::kQRotFull, dv::kKvPaged, dv::kRowWS, p, s->W * s->S, max_keys,
-                                     workspace, workspace_bytes, (hipStream_t)stream);
+    hipError_t e;
+    if (dv::use_chunk(dtype, s->S)) {
+        p.min_keys = 256;
+        e = dv::launch_chunk(dtype, dv::kQRotFull, dv::kKvPaged, p, max_keys, workspace, workspace_bytes,
+                             (hipStream_t)stream);
+    } else {
+        e = dv::launch_decode(dtype, dv::kQRotFull, dv::kKvPaged, dv::kRowWS, p, s->W * s->S, max_keys, workspace,
+                              workspace_bytes, (hipStream_t)stream);
+    }
     if (e != hipSuccess) return hip_fail(e, "dvattn_paged_sdpa launch");
     return ok();
 }
@@ -210,6 +218,8 @@ dvattn_status dvattn_varlen_paged_sdpa(int dtype, void* out, float scale, const 
 // ---------------------------------------------------------------------------
 size_t dvattn_sdpa_workspace_size(int dtype, const dvattn_shape* s, int device) {
     if (!s || !valid_dtype(dtype)) return 0;
+    if (dv::use_chunk(dtype, s->S))
+        return dv::chunk_workspace_bytes(s->W, s->S, s->Hkv, current_device(device)) + contig_table_bytes(s->F);
     return dv::decode_workspace_bytes(s->W * s->S, s->Hkv, current_device(device), dtype) +
            contig_table_bytes(s->F);
 }
@@ -283,8 +293,14 @@ dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* location
     p.bs = 1;
     p.bs_shift = 0;
     p.min_keys = 64;
-    hipError_t e = dv::launch_decode(dtype, dv::kQPre, dv::kKvContig, dv::kRowWS, p, s->W * s->S, max_keys, ws,
-                                     ws_left, (hipStream_t)stream);
+    hipError_t e;
+    if (dv::use_chunk(dtype, s->S)) {
+        p.min_keys = 256;
+        e = dv::launch_chunk(dtype, dv::kQPre, dv::kKvContig, p, max_keys, ws, ws_left, (hipStream_t)stream);
+    } else {
+        e = dv::launch_decode(dtype, dv::kQPre, dv::kKvContig, dv::kRowWS, p, s->W * s->S, max_keys, ws, ws_left,
+                              (hipStream_t)stream);
+    }
     if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa launch");
     return ok();
 }

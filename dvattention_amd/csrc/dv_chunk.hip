@@ -1,0 +1,687 @@
+// gfx950 multi-query ("chunk") attention with fused query RoPE: S >= 2 query
+// tokens per sequence that share one K/V stream (chunked prefill, speculative
+// verification).  Same operator semantics as the decode kernel
+// (src/kernels/paged_kernel_v21.cuh:17-374 and kernel_v21.cuh:17-367 in the
+// reference repository, which re-read K/V once per query token: grid.y = W*S,
+// paged_kernel_v21.cuh:391); here each K/V row is read once per block of 16
+// tokens.
+//
+//  * Workgroup = eight waves (two per SIMD) on one (sequence, 16-token block,
+//    KV head) and a contiguous range of its visible keys.  Wave w owns tokens
+//    2w, 2w+1 of the block: two 16-row query tiles (16 heads each).
+//  * K/V pages stream through a 6-stage LDS ring filled by direct-to-LDS loads
+//    (global_load_lds_dwordx4): 32 keys x 256 B of K and of V per stage, one
+//    eighth issued by each wave, completion tracked with vmcnt and a workgroup
+//    barrier.  The loads never pass through VGPRs, so five stages (80 KiB) stay
+//    in flight per CU while the waves run MFMA on the current stage.
+//  * Per stage and tile: S^T = K Q^T on 16x16x32 MFMA (8 per tile), online
+//    softmax per query row, O^T += V^T P^T (8 MFMA per tile) with V^T read by
+//    the transposing LDS read; K/V operands are read from LDS once per stage and
+//    reused by the wave's two tiles.
+//  * Rows are causal-masked per token (key l visible iff l <= locations[f,w,s]).
+//  * The balanced split / LSE merge is the decode kernel's (equal key chunks per
+//    workgroup, fp32 partial slots, dv_merge_chunk).
+#include "dv_common.h"
+#include "dv_device.h"
+
+namespace dv {
+namespace chunk {
+
+constexpr int kWaves = 8;                     // waves per workgroup
+constexpr int kThreads = kWaves * kWave;
+constexpr int kTiles = 2;                     // 16-head query tiles (tokens) per wave
+constexpr int kTokBlk = kWaves * kTiles;      // tokens per row group
+constexpr int kStages = 6;                    // K/V ring depth
+constexpr int kKvBytes = kStep * 256;         // one K (or V) stage tile: 32 keys x 256 B
+constexpr int kStageBytes = 2 * kKvBytes;     // K tile then V tile
+constexpr int kRingBytes = kStages * kStageBytes;
+constexpr int kPageCap = 2048;                // page ids cached in LDS per view sub-range
+constexpr int kDmaPerStage = 2;               // per wave: 1 x K + 1 x V (1 KiB = 4 key rows each)
+
+static __device__ __align__(16) unsigned char zrow[512];
+
+__device__ inline uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)(p));
+}
+
+// 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane.
+__device__ inline void dma16(const void* gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
+                 : "memory", "m0");
+}
+
+template <int N>
+__device__ inline void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// swizzled 16-byte piece positions inside a 256-byte key row
+__device__ inline int swz_k(int key, int piece) { return piece ^ (key & 15); }
+__device__ inline int swz_v(int key, int piece) { return piece ^ ((key & 7) << 1); }
+
+struct Range {
+    const unsigned char* k;  // K base (paged cache or this view's fragment)
+    const unsigned char* v;
+    long long off;           // paged: logical position of the view's key 0
+    long long bstride;       // contig: element offset of the sequence's batch entry
+    int L;                   // contig: tokens in the fragment tensor
+    long long lp0;           // paged: first cached logical page
+    int w, hkv;
+    int b;                   // end (exclusive) of the view-local key range
+};
+
+// Element offset of key l's row, or -1 when not visible / not addressable.
+template <int KVM>
+__device__ inline long long row_of(const DecodeParams& p, const Range& r, const int* pages, int l) {
+    if (KVM == kKvPaged) {
+        const long long pos = r.off + l;
+        long long lp;
+        if (p.bs_shift >= 0) lp = pos >> p.bs_shift;
+        else lp = pos >= 0 ? pos / p.bs : -((-pos + p.bs - 1) / p.bs);
+        const long long idx = lp - r.lp0;
+        const int page = (l < r.b && idx >= 0 && idx < kPageCap) ? pages[idx] : -1;
+        const long long rr = pos - lp * p.bs;
+        return page >= 0 ? (((long long)page * p.bs + rr) * p.Hkv + r.hkv) * kHeadDim : -1;
+    } else {
+        return l < r.b ? r.bstride + ((long long)r.hkv * r.L + l) * kHeadDim : -1;
+    }
+}
+
+// Issue this wave's eighth of stage `st` (keys [kb0, kb0+32) of the range): key
+// rows 4*wave .. 4*wave+3 of K and of V, lane -> (row lane/16, 16-byte piece).
+template <int KVM>
+__device__ inline void issue_stage(const DecodeParams& p, const Range& r, const int* pages, uint32_t ring,
+                                   int st, int kb0) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int pos = lane & 15;
+    const uint32_t sbase = ring + (uint32_t)(st % kStages) * kStageBytes;
+    const int kl = wv * 4 + (lane >> 4);
+    const long long row = row_of<KVM>(p, r, pages, kb0 + kl);
+    const int gk = swz_k(kl, pos), gv = swz_v(kl, pos);
+    const unsigned char* ka = row >= 0 ? r.k + (row + gk * 8) * 2 : zrow + gk * 16;
+    const unsigned char* va = row >= 0 ? r.v + (row + gv * 8) * 2 : zrow + gv * 16;
+    const uint32_t koff = (uint32_t)(wv * 4) * 256;
+    dma16(ka, __builtin_amdgcn_readfirstlane(sbase + koff));
+    dma16(va, __builtin_amdgcn_readfirstlane(sbase + kKvBytes + koff));
+}
+
+struct Tile {
+    f32x4 o[8];
+    float m, l;
+};
+
+template <int DT>
+__device__ inline void tile_softmax_pv(Tile& t, const f32x4& s0, const f32x4& s1, uint32_t mask, float l2scale,
+                                       const u32x4 (&vA)[8]) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4;
+    float tv[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        tv[i] = ((mask >> (g * 4 + i)) & 1u) ? s0[i] * l2scale : -DV_INF;
+        tv[4 + i] = ((mask >> (16 + g * 4 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
+    }
+    float mx = tv[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, tv[i]);
+    mx = fmaxf(mx, shfl_xor_f(mx, 16));
+    mx = fmaxf(mx, shfl_xor_f(mx, 32));
+    const float mnew = fmaxf(t.m, mx);
+    float pr[8];
+    float alpha;
+    if (mnew == -DV_INF) {
+        alpha = 1.0f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = 0.0f;
+    } else {
+        alpha = exp2f(t.m - mnew);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pr[i] = exp2f(tv[i] - mnew);
+    }
+    float ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ps += pr[i];
+    t.l = t.l * alpha + ps;
+    t.m = mnew;
+    const u32x4 pB = {pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]),
+                      pack2<DT>(pr[6], pr[7])};
+#pragma unroll
+    for (int c = 0; c < 8; ++c) t.o[c] = Tr<DT>::mma(vA[c], pB, t.o[c] * alpha);
+}
+
+// Query tiles of this wave's tokens for view f, staged through LDS (the K/V ring
+// is idle between view ranges): raw q rows arrive by direct-to-LDS loads, each
+// lane rotates whole (d, d + R/2) pairs in place (src/rope.cuh:18-51: first R/2
+// cos/sin entries, separately rounded fp32 products and sum, rounded to the
+// storage type; dims >= R untouched), then lane (g, n) reads
+// Q[n][c*32 + g*8 + 0..7] of every tile.  Wave-private LDS region: 8 KiB.
+template <int DT, int QM>
+__device__ inline void stage_q_tiles(const DecodeParams& p, unsigned char* qreg, float* csreg, int w, int tok0,
+                                     int ntile, int f, int hkv, u32x4 (&qB)[kTiles][4]) {
+#pragma clang fp contract(off)
+    using raw = typename Tr<DT>::raw;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    const uint32_t qbase = lds_addr(qreg);
+    for (int t = 0; t < ntile; ++t) {
+        const int s = tok0 + t;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int hn = i * 4 + (lane >> 4);
+            const int h = hkv * kGqa + hn;
+            const raw* q = QM == kQPre
+                               ? reinterpret_cast<const raw*>(p.q) +
+                                     ((((long long)f * p.W + w) * p.Hq + h) * p.S + s) * kHeadDim
+                               : reinterpret_cast<const raw*>(p.q) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+            dma16(q + (lane & 15) * 8, __builtin_amdgcn_readfirstlane(qbase + (uint32_t)(t * 4096 + i * 1024)));
+        }
+    }
+    const int half = p.R >> 1;
+    if (QM != kQPre) {
+        for (int t = 0; t < ntile; ++t) {
+            const long long co = (((long long)f * p.W + w) * p.S + tok0 + t) * p.R;
+            csreg[t * 128 + lane] = lane < half ? p.cosv[co + lane] : 0.0f;
+            csreg[t * 128 + 64 + lane] = lane < half ? p.sinv[co + lane] : 0.0f;
+        }
+    }
+    wait_vmcnt<0>();
+    compiler_fence();
+    if (QM != kQPre && half > 0) {
+        const int hn = lane >> 2, q4 = lane & 3;
+        for (int t = 0; t < ntile; ++t) {
+            raw* x = reinterpret_cast<raw*>(qreg + t * 4096 + hn * 256);
+            const float* cs = csreg + t * 128;
+            const float* sn = cs + 64;
+            if ((half & 7) == 0) {
+                for (int j0 = q4 * 8; j0 < half; j0 += 32) {
+                    const u32x4 a = *reinterpret_cast<const u32x4*>(x + j0);
+                    const u32x4 b = *reinterpret_cast<const u32x4*>(x + j0 + half);
+                    u32x4 ya, yb;
+#pragma unroll
+                    for (int e2 = 0; e2 < 4; ++e2) {
+                        uint32_t pa = 0, pb = 0;
+#pragma unroll
+                        for (int hl = 0; hl < 2; ++hl) {
+                            const int e = e2 * 2 + hl;
+                            const float x1 = Tr<DT>::tof((raw)((a[e2] >> (16 * hl)) & 0xffffu));
+                            const float x2 = Tr<DT>::tof((raw)((b[e2] >> (16 * hl)) & 0xffffu));
+                            const float c = cs[j0 + e], sv = sn[j0 + e];
+                            const float a1 = x1 * c, b1 = x2 * sv;
+                            const float a2 = x2 * c, b2 = x1 * sv;
+                            pa |= (uint32_t)Tr<DT>::fromf(a1 - b1) << (16 * hl);
+                            pb |= (uint32_t)Tr<DT>::fromf(a2 + b2) << (16 * hl);
+                        }
+                        ya[e2] = pa;
+                        yb[e2] = pb;
+                    }
+                    *reinterpret_cast<u32x4*>(x + j0) = ya;
+                    *reinterpret_cast<u32x4*>(x + j0 + half) = yb;
+                }
+            } else {
+                for (int j = q4; j < half; j += 4) {
+                    const float x1 = Tr<DT>::tof(x[j]), x2 = Tr<DT>::tof(x[j + half]);
+                    const float c = cs[j], sv = sn[j];
+                    const float a1 = x1 * c, b1 = x2 * sv;
+                    const float a2 = x2 * c, b2 = x1 * sv;
+                    x[j] = Tr<DT>::fromf(a1 - b1);
+                    x[j + half] = Tr<DT>::fromf(a2 + b2);
+                }
+            }
+        }
+        compiler_fence();
+    }
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t)
+        if (t < ntile)
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc)
+                qB[t][cc] = *reinterpret_cast<const u32x4*>(qreg + t * 4096 + n * 256 + (cc * 32 + g * 8) * 2);
+    compiler_fence();
+}
+
+template <int KVM>
+__device__ inline const FragDesc& frag(const DecodeParams& p, int f) {
+    return f < kMaxFragArgs ? p.frags[f] : p.frag_tab[f];
+}
+
+template <int KVM>
+__device__ inline int view_vis(const DecodeParams& p, int f, int locv) {
+    long long L = p.fl[f];
+    if (KVM == kKvContig) L = L < frag<KVM>(p, f).L ? L : frag<KVM>(p, f).L;
+    long long v = (long long)locv + 1;
+    v = v < L ? v : L;
+    return v > 0 ? (int)v : 0;
+}
+
+__device__ inline int loc_of(const DecodeParams& p, int f, int w, int s) {
+    return p.loc[((long long)f * p.W + w) * p.S + s];
+}
+
+// Visible keys of a row group: union (max) over its tokens of the per-token count.
+template <int KVM>
+__device__ inline long long group_visible(const DecodeParams& p, int rg) {
+    const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
+    const int w = rg / nsb, sb = rg - (rg / nsb) * nsb;
+    const int s1 = (sb + 1) * kTokBlk < p.S ? (sb + 1) * kTokBlk : p.S;
+    long long best = 0;
+    for (int s = sb * kTokBlk; s < s1; ++s) {
+        long long v = 0;
+        for (int f = 0; f < p.F; ++f) v += view_vis<KVM>(p, f, loc_of(p, f, w, s));
+        best = v > best ? v : best;
+    }
+    return best;
+}
+
+// One workgroup: keys [v0, v1) of row group rg for KV head hkv.
+template <int DT, int QM, int KVM>
+__device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pages, int rg, int hkv, long long v0,
+                            long long v1, bool final_out, int slot) {
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int g = lane >> 4, n = lane & 15;
+    const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
+    const int w = rg / nsb, sb = rg - (rg / nsb) * nsb;
+    const int tok0 = sb * kTokBlk + wv * kTiles;      // this wave's first token
+    const int ntile = p.S - tok0 < kTiles ? (p.S - tok0 > 0 ? p.S - tok0 : 0) : kTiles;
+    const uint32_t ring = lds_addr(smem);
+
+    Tile tl[kTiles];
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) tl[t].o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+        tl[t].m = -DV_INF;
+        tl[t].l = 0.0f;
+    }
+
+    long long P = 0, off = 0;
+    for (int f = 0; f < p.F && P < v1; ++f) {
+        // visible keys of this view for the block (union) and per tile
+        int vis_blk = 0;
+        int vis_t[kTiles];
+        const int sEnd = (sb + 1) * kTokBlk < p.S ? (sb + 1) * kTokBlk : p.S;
+        for (int s = sb * kTokBlk; s < sEnd; ++s) {
+            const int v = view_vis<KVM>(p, f, loc_of(p, f, w, s));
+            vis_blk = v > vis_blk ? v : vis_blk;
+        }
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) vis_t[t] = t < ntile ? view_vis<KVM>(p, f, loc_of(p, f, w, tok0 + t)) : 0;
+        const long long a = v0 > P ? v0 : P;
+        const long long bnd = v1 < P + vis_blk ? v1 : P + vis_blk;
+        if (a < bnd) {
+            u32x4 qB[kTiles][4];
+            // the ring is idle here (previous range drained): stage the query tiles in it
+            stage_q_tiles<DT, QM>(p, smem + wv * (kTiles * 4096),
+                                  reinterpret_cast<float*>(smem + kWaves * kTiles * 4096 + wv * kTiles * 512), w,
+                                  tok0, ntile, f, hkv, qB);
+            __syncthreads();
+            Range r;
+            r.w = w;
+            r.hkv = hkv;
+            if (KVM == kKvPaged) {
+                r.k = reinterpret_cast<const unsigned char*>(p.kc);
+                r.v = reinterpret_cast<const unsigned char*>(p.vc);
+                r.off = off;
+                r.bstride = 0;
+                r.L = 0;
+            } else {
+                const FragDesc& fd = frag<KVM>(p, f);
+                r.k = reinterpret_cast<const unsigned char*>(fd.k);
+                r.v = reinterpret_cast<const unsigned char*>(fd.v);
+                r.off = 0;
+                r.bstride = fd.bstride * w;
+                r.L = fd.L;
+            }
+            const int la = (int)(a - P), lb = (int)(bnd - P);
+            // sub-ranges whose page ids fit the LDS page cache
+            const int span = KVM == kKvPaged ? (p.bs_shift >= 0 ? (kPageCap - 2) << p.bs_shift : (kPageCap - 2) * p.bs)
+                                             : (1 << 30);
+            for (int sa = la; sa < lb; sa += span) {
+                const int sbnd = sa + span < lb ? sa + span : lb;
+                r.b = sbnd;
+                if (KVM == kKvPaged) {
+                    const long long p0 = off + sa;
+                    r.lp0 = p.bs_shift >= 0 ? (p0 >> p.bs_shift)
+                                            : (p0 >= 0 ? p0 / p.bs : -((-p0 + p.bs - 1) / p.bs));
+                    __syncthreads();
+                    for (int i = tid; i < kPageCap; i += blockDim.x) {
+                        const long long lp = r.lp0 + i;
+                        int pg = -1;
+                        if (lp >= 0 && lp < p.maxB) {
+                            pg = p.bt[(long long)w * p.maxB + lp];
+                            if (pg < 0 || pg >= p.nblocks) pg = -1;
+                        }
+                        pages[i] = pg;
+                    }
+                    __syncthreads();
+                }
+                const int nsteps = (sbnd - sa + kStep - 1) / kStep;
+                // prologue: stages 0 .. kStages-2 (past the end: rows of zeros)
+#pragma unroll
+                for (int st = 0; st < kStages - 1; ++st) issue_stage<KVM>(p, r, pages, ring, st, sa + st * kStep);
+                for (int i = 0; i < nsteps; ++i) {
+                    issue_stage<KVM>(p, r, pages, ring, i + kStages - 1, sa + (i + kStages - 1) * kStep);
+                    wait_vmcnt<kDmaPerStage * (kStages - 1)>();
+                    __builtin_amdgcn_s_barrier();
+                    const int kb0 = sa + i * kStep;
+                    const unsigned char* kt = smem + (i % kStages) * kStageBytes;
+                    const unsigned char* vt = kt + kKvBytes;
+                    // visibility of the 32 keys (page validity and range end)
+                    const bool kv_ok = row_of<KVM>(p, r, pages, kb0 + (lane & 31)) >= 0;
+                    const uint32_t okmask = (uint32_t)ballot(kv_ok && lane < 32);
+                    // K operand: lane (g, m) <- key kb*16+m, dims c*32 + g*8
+                    u32x4 kA[2][4];
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+                        for (int cc = 0; cc < 4; ++cc) {
+                            const int key = kb * 16 + n;
+                            kA[kb][cc] = *reinterpret_cast<const u32x4*>(kt + key * 256 + swz_k(key, cc * 4 + g) * 16);
+                        }
+                    // V^T operand: block lane sl -> key g*4 + sl/4 (+16), dims c*16 + (sl%4)*4
+                    u32x4 vA[8];
+                    {
+                        const int sl = lane & 15;
+                        const int k0 = g * 4 + (sl >> 2);
+                        const int k1 = k0 + 16;
+                        const int hb = (sl & 1) * 8;
+#pragma unroll
+                        for (int cc = 0; cc < 8; ++cc) {
+                            const int piece = cc * 2 + ((sl & 3) >> 1);
+                            const u32x2 a0 = lds_read_tr16(vt + k0 * 256 + swz_v(k0, piece) * 16 + hb);
+                            const u32x2 a1 = lds_read_tr16(vt + k1 * 256 + swz_v(k1, piece) * 16 + hb);
+                            vA[cc] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                        }
+                    }
+#pragma unroll
+                    for (int t = 0; t < kTiles; ++t) {
+                        if (t < ntile) {
+                            f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                            for (int cc = 0; cc < 4; ++cc) {
+                                s0 = Tr<DT>::mma(kA[0][cc], qB[t][cc], s0);
+                                s1 = Tr<DT>::mma(kA[1][cc], qB[t][cc], s1);
+                            }
+                            const int lim = vis_t[t] - kb0;
+                            const uint32_t lm = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
+                            tile_softmax_pv<DT>(tl[t], s0, s1, okmask & lm, p.l2scale, vA);
+                        }
+                    }
+                    lds_barrier();  // every wave is done with this stage before it is refilled
+                }
+                wait_vmcnt<0>();    // the trailing zero-row stages land before the ring is reused
+                __syncthreads();
+            }
+        }
+        P += vis_blk;
+        off += p.fl[f];
+    }
+
+    // epilogue: per tile, normalise and write the output or a partial slot
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) {
+        if (t >= ntile) continue;
+        float lt = tl[t].l + shfl_xor_f(tl[t].l, 16);
+        lt += shfl_xor_f(lt, 32);
+        const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+        const int s = tok0 + t;
+        const int h = hkv * kGqa + n;
+        if (final_out) {
+            using raw = typename Tr<DT>::raw;
+            raw* o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) {
+                const u32x2 pk = {pack2<DT>(tl[t].o[c][0] * inv, tl[t].o[c][1] * inv),
+                                  pack2<DT>(tl[t].o[c][2] * inv, tl[t].o[c][3] * inv)};
+                *reinterpret_cast<u32x2*>(o + c * 16 + g * 4) = pk;
+            }
+        } else {
+            const int tb = wv * kTiles + t;  // token within the block
+            float* sbase = p.part + (long long)slot * p.slot_floats;
+            float* o = sbase + (tb * kGqa + n) * kHeadDim;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(o + c * 16 + g * 4) = tl[t].o[c] * inv;
+            if (g == 0) sbase[kTokBlk * kGqa * kHeadDim + tb * kGqa + n] = lt > 0.0f ? tl[t].m + log2f(lt) : -DV_INF;
+        }
+    }
+}
+
+template <int DT, int QM, int KVM>
+__global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ long long s_scan[kWaves];
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6, lane = tid & 63;
+    int* pages = reinterpret_cast<int*>(smem + kRingBytes);
+    long long* s_pref = reinterpret_cast<long long*>(smem + kRingBytes + kPageCap * 4);
+    const int NHG = p.Hkv;  // one KV head per workgroup
+
+    // 1. visible keys per row group -> exclusive prefix sums
+    const int nrows = p.nrows;
+    const int per = (nrows + kThreads - 1) / kThreads;
+    const int r0 = tid * per;
+    const int r1 = r0 + per < nrows ? r0 + per : nrows;
+    long long mine = 0;
+    for (int r = r0; r < r1; ++r) mine += group_visible<KVM>(p, p.row_begin + r);
+    long long incl = mine;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const long long o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) s_scan[wv] = incl;
+    __syncthreads();
+    long long before = 0;
+    for (int i = 0; i < wv; ++i) before += s_scan[i];
+    long long run = before + incl - mine;
+    for (int r = r0; r < r1; ++r) {
+        s_pref[r] = run;
+        run += group_visible<KVM>(p, p.row_begin + r);
+    }
+    long long total = 0;
+    for (int i = 0; i < kWaves; ++i) total += s_scan[i];
+    if (tid == 0) s_pref[nrows] = total;
+    __syncthreads();
+
+    // 2. equal chunks of the (row group, KV head) segments laid end to end
+    const long long Wk = total * NHG;
+    const long long ng = (Wk + p.min_keys - 1) / p.min_keys;
+    const int geff = Wk == 0 ? 0 : (int)(ng < p.nwg ? ng : p.nwg);
+    const long long chunk = geff ? (Wk + geff - 1) / geff : 1;
+    if (blockIdx.x == 0) {
+        for (int sg = tid; sg < nrows * NHG; sg += blockDim.x) {
+            const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
+            const long long V = s_pref[r + 1] - s_pref[r];
+            int base = 0, cnt = 0;
+            if (V > 0) {
+                const long long stt = NHG * s_pref[r] + hg * V;
+                const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
+                cnt = (int)(gl - gf + 1);
+                base = (int)gf + sg;
+            }
+            p.dir[2 * sg] = base;
+            p.dir[2 * sg + 1] = cnt;
+        }
+    }
+    const int gidx = blockIdx.x;
+    if (gidx >= geff) return;
+    long long u = gidx * chunk;
+    const long long uend = u + chunk < Wk ? u + chunk : Wk;
+    int lo = 0, hi = nrows - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (NHG * s_pref[mid] <= u) lo = mid;
+        else hi = mid - 1;
+    }
+    int r = lo;
+    while (u < uend && r < nrows) {
+        const long long rs = NHG * s_pref[r];
+        const long long V = s_pref[r + 1] - s_pref[r];
+        if (V == 0 || u >= rs + NHG * V) {
+            ++r;
+            continue;
+        }
+        const long long rel = u - rs;
+        const int hg = (int)(rel / V);
+        const long long v0 = rel - hg * V;
+        const long long segend = (long long)(hg + 1) * V;
+        const long long lim = (uend - rs < segend ? uend - rs : segend) - (long long)hg * V;
+        const int sg = r * NHG + hg;
+        const long long stt = rs + hg * V;
+        const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
+        chunk_piece<DT, QM, KVM>(p, smem, pages, p.row_begin + r, hg, v0, lim, gl == gf, sg + gidx);
+        u = stt + lim;
+    }
+}
+
+// Block (segment, token of the block): thread t -> head t/16, dims [(t%16)*8, +8).
+template <int DT>
+__global__ __launch_bounds__(256) void dv_merge_chunk(const DecodeParams p) {
+    using raw = typename Tr<DT>::raw;
+    const int sg = blockIdx.x / kTokBlk;
+    const int tb = blockIdx.x - sg * kTokBlk;
+    const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
+    if (cnt == 1) return;
+    const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
+    const int NHG = p.Hkv;
+    const int r = sg / NHG, hkv = sg - (sg / NHG) * NHG;
+    const int rg = p.row_begin + r;
+    const int w = rg / nsb, sb = rg - (rg / nsb) * nsb;
+    const int s = sb * kTokBlk + tb;
+    if (s >= p.S) return;
+    const int tid = threadIdx.x;
+    const int n = tid >> 4;
+    const int d = (tid & 15) * 8;
+    const int h = hkv * kGqa + n;
+    raw* o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim + d;
+    const int j = tb * kGqa + n;
+    const int lse_off = kTokBlk * kGqa * kHeadDim + j;
+    const int val_off = j * kHeadDim + d;
+    float m = -DV_INF, wsum = 0.0f;
+    float acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    constexpr int kB = 8;
+    for (int k0 = 0; k0 < cnt; k0 += kB) {
+        float lse[kB];
+        f32x4 v0[kB], v1[kB];
+#pragma unroll
+        for (int i = 0; i < kB; ++i) {
+            const bool in = k0 + i < cnt;
+            const float* sp = p.part + (long long)(base + (in ? k0 + i : k0)) * p.slot_floats;
+            lse[i] = in ? sp[lse_off] : -DV_INF;
+            v0[i] = ld16f(sp + val_off);
+            v1[i] = ld16f(sp + val_off + 4);
+        }
+        float bm = m;
+#pragma unroll
+        for (int i = 0; i < kB; ++i) bm = fmaxf(bm, lse[i]);
+        if (bm == -DV_INF) continue;
+        const float sc = exp2f(m - bm);
+        wsum *= sc;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[e] *= sc;
+#pragma unroll
+        for (int i = 0; i < kB; ++i) {
+            const float wgt = exp2f(lse[i] - bm);
+            wsum += wgt;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[e] += wgt * v0[i][e];
+                acc[4 + e] += wgt * v1[i][e];
+            }
+        }
+        m = bm;
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+    const u32x4 pk = {pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv),
+                      pack2<DT>(acc[4] * inv, acc[5] * inv), pack2<DT>(acc[6] * inv, acc[7] * inv)};
+    *reinterpret_cast<u32x4*>(o) = pk;
+}
+
+size_t lds_bytes(int nrows) {
+    return (size_t)kRingBytes + (size_t)kPageCap * 4 + (size_t)(nrows + 1) * sizeof(long long);
+}
+
+template <int DT, int QM, int KVM>
+hipError_t launch(DecodeParams p, int cus, long long cap, hipStream_t stream) {
+    static bool attr = false;
+    if (!attr) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_chunk<DT, QM, KVM>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes(kMaxRows));
+        if (e != hipSuccess) return e;
+        attr = true;
+    }
+    const size_t lds = lds_bytes(p.nrows);
+    long long nwg = cus;  // one eight-wave workgroup per CU (LDS ring 96 KiB)
+    if (nwg > cap) nwg = cap;
+    p.nwg = nwg < 1 ? 1 : (int)nwg;
+    hipLaunchKernelGGL((dv_chunk<DT, QM, KVM>), dim3(p.nwg), dim3(kThreads), lds, stream, p);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    hipLaunchKernelGGL((dv_merge_chunk<DT>), dim3(p.nrows * p.Hkv * kTokBlk), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace chunk
+
+namespace {
+int chunk_cus(int device) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c <= 0) c = 256;
+    return c;
+}
+}  // namespace
+
+size_t chunk_workspace_bytes(int W, int S, int Hkv, int device) {
+    if (W <= 0 || S <= 0 || Hkv <= 0) return 0;
+    const long long groups = (long long)W * ((S + chunk::kTokBlk - 1) / chunk::kTokBlk);
+    const long long rows = groups < kMaxRows ? groups : kMaxRows;
+    const long long nseg = rows * Hkv;
+    const long long slot_floats = (long long)chunk::kTokBlk * kGqa * (kHeadDim + 1);
+    const long long slots = chunk_cus(device) + nseg;
+    size_t bytes = (size_t)(slots * slot_floats * 4);
+    bytes = (bytes + 255) & ~(size_t)255;
+    bytes += (size_t)(nseg * 2 * 4);
+    return bytes;
+}
+
+hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& base, long long max_keys_per_group,
+                        void* workspace, size_t ws_bytes, hipStream_t stream) {
+    if (base.W <= 0 || base.S <= 0 || base.Hkv <= 0) return hipSuccess;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    const int cus = chunk_cus(device);
+    DecodeParams p = base;
+    p.hpw = 1;
+    p.slot_floats = chunk::kTokBlk * kGqa * (kHeadDim + 1);
+    const long long groups_total = (long long)p.W * ((p.S + chunk::kTokBlk - 1) / chunk::kTokBlk);
+    const long long rows_cap = groups_total < kMaxRows ? groups_total : kMaxRows;
+    const long long nseg_cap = rows_cap * p.Hkv;
+    size_t part_bytes = (size_t)((cus + nseg_cap) * p.slot_floats * 4);
+    part_bytes = (part_bytes + 255) & ~(size_t)255;
+    if (ws_bytes < part_bytes + (size_t)nseg_cap * 2 * 4) return hipErrorInvalidValue;
+    p.part = reinterpret_cast<float*>(workspace);
+    p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
+    for (long long g0 = 0; g0 < groups_total; g0 += kMaxRows) {
+        p.row_begin = (int)g0;
+        p.nrows = (int)(groups_total - g0 < kMaxRows ? groups_total - g0 : kMaxRows);
+        const long long cap = ((long long)p.nrows * p.Hkv * max_keys_per_group + p.min_keys - 1) / p.min_keys;
+        if (dtype == kBF16 && qmode == kQRotFull && kvmode == kKvPaged)
+            e = chunk::launch<kBF16, kQRotFull, kKvPaged>(p, cus, cap, stream);
+        else if (dtype == kF16 && qmode == kQRotFull && kvmode == kKvPaged)
+            e = chunk::launch<kF16, kQRotFull, kKvPaged>(p, cus, cap, stream);
+        else if (dtype == kBF16 && qmode == kQPre && kvmode == kKvContig)
+            e = chunk::launch<kBF16, kQPre, kKvContig>(p, cus, cap, stream);
+        else if (dtype == kF16 && qmode == kQPre && kvmode == kKvContig)
+            e = chunk::launch<kF16, kQPre, kKvContig>(p, cus, cap, stream);
+        else
+            e = hipErrorInvalidValue;
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace dv

@@ -91,6 +91,13 @@ hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const De
                          int nrows_total, long long max_keys_per_row, void* workspace, size_t ws_bytes,
                          hipStream_t stream);
 hipError_t launch_rope(int dtype, const RopeParams& p, hipStream_t stream);
+
+// Multi-query path (S >= 2 tokens per sequence, 16-bit types): K/V read once per
+// block of 16 tokens.  Rows of DecodeParams are (sequence, 16-token block) groups.
+inline bool use_chunk(int dtype, int S) { return S >= 2 && dtype != kF32; }
+size_t chunk_workspace_bytes(int W, int S, int Hkv, int device);
+hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& base, long long max_keys_per_group,
+                        void* workspace, size_t ws_bytes, hipStream_t stream);
 // Which runtime call produced the last error returned by launch_decode (this thread).
 const char* last_hip_site();
 

@@ -113,6 +113,10 @@ PAGED_CASES = [
     (1, 2, 2, 1, 64, [300], 0),
     (2, 1, 4, 2, 1, [20, 9], 16),
     (4, 2, 1, 3, 8, [15, 64, 1, 40], 64),
+    # multi-query rows (S >= 2 takes the chunk kernel for 16-bit types)
+    (1, 2, 16, 2, 16, [600], 32),
+    (2, 1, 17, 1, 16, [90, 300], 128),
+    (1, 3, 5, 8, 64, [700], 64),
 ]
 
 
@@ -125,6 +129,17 @@ def test_paged_vs_oracle(dv, gpu, dtype, case):
     out = run_paged(dv, d, scale, gpu)
     ref = O.paged_sdpa(scale, **d)
     close(out, ref, dtype, f"paged {case}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_chunk_causal_block(dv, gpu, dtype):
+    # config-5 shape in miniature: 16 new tokens, causal inside the chunk, several pieces per segment
+    W, Hkv, S, bs, prior = 3, 2, 16, 16, 2000
+    L = prior + S
+    loc = (prior + np.arange(S))[None, None, :].repeat(W, 1).astype(np.int32)
+    d = rand_paged(1, W, S, Hkv, bs, [L], 32, dtype, seed=21, loc=loc)
+    out = run_paged(dv, d, 0.1, gpu)
+    close(out, O.paged_sdpa(0.1, **d), dtype, "chunk")
 
 
 def test_paged_through_c_abi_matches_torch_op(dv, gpu):
