@@ -40,21 +40,6 @@ constexpr int kDmaPerStage = 2;               // per wave: 1 x K + 1 x V (1 KiB 
 
 static __device__ __align__(16) unsigned char zrow[512];
 
-__device__ inline uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)(p));
-}
-
-// 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane.
-__device__ inline void dma16(const void* gptr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
-                 : "memory", "m0");
-}
-
-template <int N>
-__device__ inline void wait_vmcnt() {
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // swizzled 16-byte piece positions inside a 256-byte key row

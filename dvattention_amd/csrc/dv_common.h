@@ -13,7 +13,7 @@ constexpr int kWave = 64;         // CDNA wavefront width
 constexpr int kGqa = 16;          // query heads per KV head (reference hard-wires 16)
 constexpr int kHeadDim = 128;     // E == Ev == 128 (reference hard-wires 128)
 constexpr int kStep = 32;         // keys per wave per pipeline step (two 16-key MFMA blocks)
-constexpr int kMaxRows = 4096;    // query rows per decode launch (schedule prefix lives in LDS)
+constexpr int kMaxRows = 2048;    // query rows per decode launch (schedule prefix lives in LDS)
 constexpr int kMaxFragArgs = 16;  // contiguous views passed in kernel arguments
 constexpr int kMaxWavesPerWg = 4; // KV heads per workgroup (one wave per KV head)
 

@@ -145,37 +145,20 @@ __device__ inline long long kv_row(const DecodeParams& p, const KvCtx& c, const 
     }
 }
 
-// 16-bit types: one step = keys [l, l+32) as two 16-key MFMA blocks.
-// Lane (g = lane/16, m = lane%16) loads dims [c*32 + g*8, +8), c = 0..3, of keys
-// m and 16+m: the A operand of S^T = K Q^T, and the V rows it stages in LDS.
-struct Kv16 {
-    u32x4 k[2][4];
-    u32x4 v[2][4];
-    uint32_t mask;  // bit j: key l+j visible
-};
-
 // Rows of zeros that invisible keys load from, so every lane issues the same
 // loads (no divergent branches around the memory instructions).
 __device__ __align__(16) unsigned char g_zero_row[512];
 
-template <int DT, int KVM>
-__device__ inline void issue16(const DecodeParams& p, const KvCtx& c, const PageWin& win, Kv16& b,
-                               int l, int l1) {
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, m = lane & 15;
-    bool okb[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-        const long long row = kv_row<KVM>(p, c, win, l + kb * 16 + m, l1);
-        okb[kb] = row >= 0;
-        const unsigned char* kp = okb[kb] ? c.k + (row + g * 8) * 2 : g_zero_row + g * 16;
-        const unsigned char* vp = okb[kb] ? c.v + (row + g * 8) * 2 : g_zero_row + g * 16;
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) b.k[kb][cc] = ld16(kp + cc * 64);
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) b.v[kb][cc] = ld16(vp + cc * 64);
+// Logical page and in-page offset of a logical key position (32-bit, as the
+// reference's absolute_key_pos, paged_kernel_v21.cuh:103-104).
+__device__ inline void page_split(const DecodeParams& p, uint32_t pos, uint32_t& lp, uint32_t& r) {
+    if (p.bs_shift >= 0) {
+        lp = pos >> p.bs_shift;
+        r = pos & ((1u << p.bs_shift) - 1u);
+    } else {
+        lp = pos / (uint32_t)p.bs;
+        r = pos - lp * (uint32_t)p.bs;
     }
-    b.mask = (uint32_t)(ballot(okb[0]) & 0xffffu) | ((uint32_t)(ballot(okb[1]) & 0xffffu) << 16);
 }
 
 struct SoftState {
@@ -202,60 +185,22 @@ __device__ inline void softmax_step(SoftState& st, const f32x4& s0, const f32x4&
     mx = fmaxf(mx, shfl_xor_f(mx, 16));
     mx = fmaxf(mx, shfl_xor_f(mx, 32));
     const float mnew = fmaxf(st.m, mx);
-    float alpha;
-    if (mnew == -DV_INF) {
-        alpha = 1.0f;
+    // The accumulator is rescaled only when some head's running max grows, which
+    // after the first steps is rare; otherwise alpha == 1 for every lane.
+    if (ballot(mnew > st.m)) {
+        const float alpha = mnew == -DV_INF ? 1.0f : exp2f(st.m - mnew);
+        st.l *= alpha;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = 0.0f;
-    } else {
-        alpha = exp2f(st.m - mnew);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = exp2f(t[i] - mnew);
+        for (int c = 0; c < 8; ++c) st.o[c] *= alpha;
+        st.m = mnew;
     }
     float ps = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ps += pr[i];
-    st.l = st.l * alpha + ps;
-    st.m = mnew;
-#pragma unroll
-    for (int c = 0; c < 8; ++c) st.o[c] *= alpha;
-}
-
-template <int DT>
-__device__ inline void compute16(SoftState& st, const Kv16& b, const u32x4 (&qB)[4], unsigned char* vt,
-                                 float l2scale) {
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, m = lane & 15;
-    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-        s0 = Tr<DT>::mma(b.k[0][cc], qB[cc], s0);
-        s1 = Tr<DT>::mma(b.k[1][cc], qB[cc], s1);
+    for (int i = 0; i < 8; ++i) {
+        pr[i] = mnew == -DV_INF ? 0.0f : exp2f(t[i] - mnew);
+        ps += pr[i];
     }
-    // stage V rows: key kb*16+m, bytes [c*64 + g*16, +16)
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc)
-            *reinterpret_cast<u32x4*>(vt + (kb * 16 + m) * kVtStride16 + cc * 64 + g * 16) = b.v[kb][cc];
-    compiler_fence();
-    float pr[8];
-    softmax_step(st, s0, s1, b.mask, l2scale, pr);
-    // P^T operand: k = g*8 + jj <-> key (jj/4)*16 + g*4 + jj%4
-    const u32x4 pB = {pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]),
-                      pack2<DT>(pr[6], pr[7])};
-    // V^T operand for dims [c*16, +16): block lane sl points at key g*4 + sl/4,
-    // dims c*16 + (sl%4)*4; the transposed read hands lane n V[g*4+j][c*16+n].
-    const int sl = lane & 15;
-    const unsigned char* vbase = vt + (g * 4 + (sl >> 2)) * kVtStride16 + (sl & 3) * 8;
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-        const u32x2 a0 = lds_read_tr16(vbase + cc * 32);
-        const u32x2 a1 = lds_read_tr16(vbase + 16 * kVtStride16 + cc * 32);
-        const u32x4 vA = {a0[0], a0[1], a1[0], a1[1]};
-        st.o[cc] = Tr<DT>::mma(vA, pB, st.o[cc]);
-    }
-    compiler_fence();
+    st.l += ps;
 }
 
 // fp32: lane (g, m) loads dims [c*16 + g*4, +4), c = 0..7, of keys m and 16+m.
@@ -443,26 +388,14 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
                 c.bstride = fd.bstride * w;
                 c.L = fd.L;
             }
-            if constexpr (DT == kF32) {
-                f32x4 qB[8];
-                load_q32<QM, RM>(p, row, f, hkv, qB);
-                for (int l = l0; l < l1; l += kStep) {
-                    Kv32 b;
-                    window_update<DT, KVM>(p, c, win, l, l1);
-                    issue32<KVM>(p, c, win, b, l, l1);
-                    compute32(st, b, qB, vt, p.l2scale);
-                }
-            } else {
-                u32x4 qB[4];
-                load_q16<DT, QM, RM>(p, row, f, hkv, qB);
-                // One 32-key step in flight per wave; with two workgroups of four waves per
-                // CU, eight waves interleave their loads and MFMA work.
-                for (int l = l0; l < l1; l += kStep) {
-                    Kv16 b;
-                    window_update<DT, KVM>(p, c, win, l, l1);
-                    issue16<DT, KVM>(p, c, win, b, l, l1);
-                    compute16<DT>(st, b, qB, vt, p.l2scale);
-                }
+            static_assert(DT == kF32, "16-bit types use dv_stream");
+            f32x4 qB[8];
+            load_q32<QM, RM>(p, row, f, hkv, qB);
+            for (int l = l0; l < l1; l += kStep) {
+                Kv32 b;
+                window_update<DT, KVM>(p, c, win, l, l1);
+                issue32<KVM>(p, c, win, b, l, l1);
+                compute32(st, b, qB, vt, p.l2scale);
             }
         }
         P += vis;
@@ -505,18 +438,21 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
     }
 }
 
-// ---- the decode kernel ----------------------------------------------------------
+// ---- work schedule ----------------------------------------------------------------
 
-template <int DT, int QM, int KVM, int RM>
-__global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ long long s_scan[4];
+// Every workgroup computes the same schedule from locations / fragment_lengths:
+// per-row visible key counts -> exclusive prefix sums in LDS (s_pref, nrows + 1
+// entries); all (row, KV-head-group) segments of visible keys laid end to end and
+// cut into equal contiguous chunks, one per workgroup.  Workgroup 0 also writes
+// the merge directory (segment -> first partial slot, piece count).  Then
+// piece(row, head_group, v0, v1, final, slot) runs for each segment piece of this
+// workgroup's chunk; `final` means the segment has no other piece.
+template <int KVM, int RM, class PieceFn>
+__device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, long long* s_scan, PieceFn&& piece) {
     const int tid = threadIdx.x;
     const int wv = tid >> 6;
     const int nthreads = blockDim.x;
-    const int HPW = p.hpw;
-    const int NHG = p.Hkv / HPW;
-    long long* s_pref = reinterpret_cast<long long*>(smem + HPW * vt_bytes<DT>());
+    const int NHG = p.Hkv / p.hpw;
 
     // 1. per-row visible key counts -> exclusive prefix sums in LDS
     const int nrows = p.nrows;
@@ -525,7 +461,6 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
     const int r1 = r0 + per < nrows ? r0 + per : nrows;
     long long mine = 0;
     for (int r = r0; r < r1; ++r) mine += row_visible<KVM, RM>(p, p.row_begin + r);
-    // wave inclusive scan
     const int lane = tid & 63;
     long long incl = mine;
 #pragma unroll
@@ -554,7 +489,6 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
                                                                                 : p.nwg);
     const long long chunk = geff ? (Wk + geff - 1) / geff : 1;
 
-    // directory: segment sg = r*NHG + hg -> {first slot, piece count}
     if (blockIdx.x == 0) {
         for (int sg = tid; sg < nrows * NHG; sg += nthreads) {
             const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
@@ -583,7 +517,6 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
         else hi = mid - 1;
     }
     int r = lo;
-    unsigned char* vt = smem + wv * vt_bytes<DT>();
     while (u < uend && r < nrows) {
         const long long rs = NHG * s_pref[r];
         const long long V = s_pref[r + 1] - s_pref[r];
@@ -601,12 +534,289 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
         const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
         const int cnt = (int)(gl - gf + 1);
         const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
-        if (wv < HPW) {
-            process_piece<DT, QM, KVM, RM>(p, vt, p.row_begin + r, hg * HPW + wv, v0, lim, cnt == 1, slot,
-                                           wv);
-        }
+        piece(p.row_begin + r, hg, v0, lim, cnt == 1, slot);
         u = stt + lim;
     }
+}
+
+// ---- the fp32 decode kernel --------------------------------------------------------
+
+template <int DT, int QM, int KVM, int RM>
+__global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ long long s_scan[4];
+    const int wv = threadIdx.x >> 6;
+    const int HPW = p.hpw;
+    long long* s_pref = reinterpret_cast<long long*>(smem + HPW * vt_bytes<DT>());
+    unsigned char* vt = smem + wv * vt_bytes<DT>();
+    run_schedule<KVM, RM>(p, s_pref, s_scan, [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
+        if (wv < HPW) process_piece<DT, QM, KVM, RM>(p, vt, row, hg * HPW + wv, v0, v1, fin, slot, wv);
+    });
+}
+
+// ---- the 16-bit streaming decode kernel --------------------------------------------
+//
+// Same operator and schedule as dv_decode; K/V reach LDS by direct-to-LDS loads
+// (global_load_lds_dwordx4) into a two-stage ring private to each wave, so no
+// VGPRs are held by loads in flight and the next stage streams in while the
+// current one runs on MFMA.  A stage is 32 keys: an 8 KiB K tile and an 8 KiB V
+// tile, each key row 256 B with its 16-byte pieces XOR-swizzled (K: piece ^
+// (key & 15) for the row-wise ds_read_b128 of the MFMA A operand; V: piece ^
+// ((key & 7) << 1) for the transposing reads) so both reads are free of bank
+// conflicts.  Completion is tracked with explicit vmcnt waits (16 loads per
+// stage and wave); the physical pages of the current key range sit in a
+// per-wave LDS page cache, so the loop issues no other vector-memory operation.
+
+namespace stream {
+
+constexpr int kTile = kStep * 256;           // one K (or V) stage tile: 32 keys x 256 B
+constexpr int kStage = 2 * kTile;            // K tile then V tile
+constexpr int kRing = 2;                     // stages per wave
+constexpr int kPc = 512;                     // page ids cached per wave
+constexpr int kWaveLds = kRing * kStage + kPc * 4;
+
+struct View {
+    const unsigned char* k;  // paged: the cache; contiguous: K row 0 of (batch entry, head)
+    const unsigned char* v;
+    int off;                 // paged: logical position of the view's key 0
+    int lp0;                 // paged: logical page of page-cache entry 0
+    int b;                   // end (exclusive) of the current view-local key range
+    int hkv;
+};
+
+// Issue the 16 direct-to-LDS loads of the stage holding keys [l, l+32) into the
+// ring slot at LDS address sbase.  Load i moves key rows 4i .. 4i+3: lane ->
+// (row lane/16, swizzled piece).  Returns the visibility mask of the 32 keys.
+template <int KVM>
+__device__ inline uint32_t issue(const DecodeParams& p, const View& v, const int* pc, uint32_t sbase, int l) {
+    const int lane = threadIdx.x & 63;
+    const int c16 = lane & 15, sub = lane >> 4;
+    // addresses of the 8 key rows first (page-cache reads batched), then the loads
+    const unsigned char* ka[8];
+    const unsigned char* va[8];
+    bool ok[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int kk = i * 4 + sub;
+        const int key = l + kk;
+        unsigned long long boff;
+        if (KVM == kKvPaged) {
+            const int pos = v.off + key;
+            uint32_t lp, r;
+            page_split(p, pos > 0 ? (uint32_t)pos : 0u, lp, r);
+            const uint32_t idx = lp - (uint32_t)v.lp0;
+            const bool in = key < v.b && pos >= 0 && idx < (uint32_t)kPc;
+            const int page = in ? pc[in ? idx : 0u] : -1;
+            ok[i] = page >= 0;
+            const uint32_t rowidx = ((uint32_t)page * (uint32_t)p.bs + r) * (uint32_t)p.Hkv + (uint32_t)v.hkv;
+            boff = (unsigned long long)rowidx << 8;
+        } else {
+            ok[i] = key < v.b;
+            boff = (unsigned long long)(uint32_t)key << 8;
+        }
+        const int gk = c16 ^ (kk & 15), gv = c16 ^ ((kk & 7) << 1);
+        ka[i] = ok[i] ? v.k + boff + gk * 16 : g_zero_row + gk * 16;
+        va[i] = ok[i] ? v.v + boff + gv * 16 : g_zero_row + gv * 16;
+    }
+    uint32_t mask = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        dma16(ka[i], sbase + (uint32_t)(i * 1024));
+        dma16(va[i], sbase + (uint32_t)(kTile + i * 1024));
+        const uint64_t bl = ballot(ok[i]);
+        const uint32_t bits = (uint32_t)(bl & 1u) | (uint32_t)((bl >> 15) & 2u) | (uint32_t)((bl >> 30) & 4u) |
+                              (uint32_t)((bl >> 45) & 8u);
+        mask |= bits << (i * 4);
+    }
+    return mask;
+}
+
+// One stage on MFMA: S^T = K Q^T from the K tile, online softmax, O^T += V^T P^T
+// with V^T from the transposing reads of the V tile.
+template <int DT>
+__device__ inline void compute(SoftState& st, const unsigned char* kt, const unsigned char* vt, uint32_t mask,
+                               const u32x4 (&qB)[4], float l2scale) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    u32x4 kA[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const int key = kb * 16 + n;
+            kA[kb][cc] = *reinterpret_cast<const u32x4*>(kt + key * 256 + (((cc * 4 + g) ^ (key & 15)) * 16));
+        }
+    f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        s0 = Tr<DT>::mma(kA[0][cc], qB[cc], s0);
+        s1 = Tr<DT>::mma(kA[1][cc], qB[cc], s1);
+    }
+    // V^T operand for dims [c*16, +16): block lane sl -> key g*4 + sl/4 (and +16),
+    // dims c*16 + (sl%4)*4; the transposed read hands lane n V[key][c*16 + n].
+    u32x4 vA[8];
+    {
+        const int sl = lane & 15;
+        const int k0 = g * 4 + (sl >> 2);
+        const int k1 = k0 + 16;
+        const int hb = (sl & 1) * 8;
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) {
+            const int piece = cc * 2 + ((sl & 3) >> 1);
+            const u32x2 a0 = lds_read_tr16(vt + k0 * 256 + ((piece ^ ((k0 & 7) << 1)) * 16) + hb);
+            const u32x2 a1 = lds_read_tr16(vt + k1 * 256 + ((piece ^ ((k1 & 7) << 1)) * 16) + hb);
+            vA[cc] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+        }
+    }
+    float pr[8];
+    softmax_step(st, s0, s1, mask, l2scale, pr);
+    // P^T operand: k = g*8 + jj <-> key (jj/4)*16 + g*4 + jj%4
+    const u32x4 pB = {pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]),
+                      pack2<DT>(pr[6], pr[7])};
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) st.o[cc] = Tr<DT>::mma(vA[cc], pB, st.o[cc]);
+}
+
+// One wave: KV head hkv over visible keys [v0, v1) of one row.  wlds: this
+// wave's LDS (ring, then page cache).
+template <int DT, int QM, int KVM, int RM>
+__device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int hkv, long long v0, long long v1,
+                      bool final_out, int slot, int wv) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    const uint32_t ring = __builtin_amdgcn_readfirstlane(lds_addr(wlds));
+    int* pc = reinterpret_cast<int*>(wlds + kRing * kStage);
+
+    int w;
+    if (RM == kRowVarlen) w = varlen_seq(p, row);
+    else w = row / p.S;
+
+    SoftState st;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) st.o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    st.m = -DV_INF;
+    st.l = 0.0f;
+
+    long long P = 0;    // visible keys of the earlier views
+    long long off = 0;  // logical position of view f (paged): sum of earlier fragment_lengths
+    for (int f = 0; f < p.F && P < v1; ++f) {
+        const int vis = view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
+        const long long a = v0 > P ? v0 : P;
+        const long long bnd = v1 < P + vis ? v1 : P + vis;
+        if (a < bnd) {
+            const int l0 = (int)(a - P), l1 = (int)(bnd - P);
+            View v;
+            v.hkv = hkv;
+            if (KVM == kKvPaged) {
+                v.k = reinterpret_cast<const unsigned char*>(p.kc);
+                v.v = reinterpret_cast<const unsigned char*>(p.vc);
+                v.off = (int)off;
+            } else {
+                const FragDesc& fd = frag<KVM>(p, f);
+                const long long base = (fd.bstride * w + (long long)hkv * fd.L * kHeadDim) * 2;
+                v.k = reinterpret_cast<const unsigned char*>(fd.k) + base;
+                v.v = reinterpret_cast<const unsigned char*>(fd.v) + base;
+                v.off = 0;
+            }
+            v.lp0 = 0;
+            u32x4 qB[4];
+            bool have_q = false;
+            // sub-ranges whose pages fit the page cache
+            const long long span = KVM == kKvPaged ? (long long)(kPc - 1) * p.bs : (1ll << 30);
+            for (int sa = l0; sa < l1;) {
+                const int sb = (long long)l1 - sa > span ? (int)(sa + span) : l1;
+                v.b = sb;
+                if (KVM == kKvPaged) {
+                    uint32_t lpa, lpz, r;
+                    const int pa = v.off + sa, pz = v.off + sb - 1;
+                    page_split(p, pa > 0 ? (uint32_t)pa : 0u, lpa, r);
+                    page_split(p, pz > 0 ? (uint32_t)pz : 0u, lpz, r);
+                    v.lp0 = (int)lpa;
+                    const int need = (int)(lpz - lpa) + 1;
+                    const int* bt = p.bt + (long long)w * p.maxB;
+                    for (int i = lane; i < need; i += kWave) {
+                        const uint32_t lp = lpa + (uint32_t)i;
+                        int pg = lp < (uint32_t)p.maxB ? bt[lp] : -1;
+                        if (pg < 0 || pg >= p.nblocks) pg = -1;
+                        pc[i] = pg;
+                    }
+                }
+                const int n_st = (sb - sa + kStep - 1) / kStep;
+                uint32_t m0 = issue<KVM>(p, v, pc, ring, sa);
+                uint32_t m1 = 0;
+                if (n_st > 1) m1 = issue<KVM>(p, v, pc, ring + kStage, sa + kStep);
+                if (!have_q) {
+                    // rotated once per (row, view) while the first stages are in flight
+                    load_q16<DT, QM, RM>(p, row, f, hkv, qB);
+                    // settle the query loads here: a load still pending in qB at the loop
+                    // would make the compiler wait for all vector memory in every step
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) asm volatile("" : "+v"(qB[cc]));
+                    have_q = true;
+                }
+                for (int s = 0; s < n_st; ++s) {
+                    if (s + 1 < n_st) wait_vmcnt<16>();
+                    else wait_vmcnt<0>();
+                    const unsigned char* kt = wlds + (s & 1) * kStage;
+                    compute<DT>(st, kt, kt + kTile, (s & 1) ? m1 : m0, qB, p.l2scale);
+                    if (s + 2 < n_st) {
+                        lds_wait();  // the slot's reads are complete before it is refilled
+                        const uint32_t mk = issue<KVM>(p, v, pc, ring + (uint32_t)((s & 1) * kStage),
+                                                       sa + (s + 2) * kStep);
+                        if (s & 1) m1 = mk;
+                        else m0 = mk;
+                    }
+                }
+                lds_wait();
+                sa = sb;
+            }
+        }
+        P += vis;
+        off += p.fl[f];
+    }
+
+    // epilogue: total over the four lane groups, normalise, base-2 LSE
+    float lt = st.l + shfl_xor_f(st.l, 16);
+    lt += shfl_xor_f(lt, 32);
+    const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
+    const int h = hkv * kGqa + n;
+    if (final_out) {
+        using raw = typename Tr<DT>::raw;
+        raw* o;
+        if (RM == kRowVarlen) {
+            o = reinterpret_cast<raw*>(p.out) + ((long long)row * p.Hq + h) * kHeadDim;
+        } else {
+            const int s = row - w * p.S;
+            o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+        }
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const u32x2 pk = {pack2<DT>(st.o[c][0] * inv, st.o[c][1] * inv),
+                              pack2<DT>(st.o[c][2] * inv, st.o[c][3] * inv)};
+            *reinterpret_cast<u32x2*>(o + c * 16 + g * 4) = pk;
+        }
+    } else {
+        float* sbase = p.part + (long long)slot * p.slot_floats;
+        float* o = sbase + (wv * kGqa + n) * kHeadDim;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(o + c * 16 + g * 4) = st.o[c] * inv;
+        if (g == 0) sbase[p.hpw * kGqa * kHeadDim + wv * kGqa + n] = lt > 0.0f ? st.m + log2f(lt) : -DV_INF;
+    }
+}
+
+}  // namespace stream
+
+template <int DT, int QM, int KVM, int RM>
+__global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ long long s_scan[4];
+    const int wv = threadIdx.x >> 6;
+    const int HPW = p.hpw;
+    long long* s_pref = reinterpret_cast<long long*>(smem + HPW * stream::kWaveLds);
+    unsigned char* wlds = smem + wv * stream::kWaveLds;
+    run_schedule<KVM, RM>(p, s_pref, s_scan, [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
+        if (wv < HPW) stream::piece<DT, QM, KVM, RM>(p, wlds, row, hg * HPW + wv, v0, v1, fin, slot, wv);
+    });
 }
 
 // ---- split merge -------------------------------------------------------------------
@@ -726,6 +936,19 @@ int pick_hpw(int Hkv) {
 // workgroups per CU such that about eight waves share a CU
 int wgs_per_cu(int hpw) { return 8 / hpw; }
 
+// The decode kernel for a dtype: the LDS-streaming kernel for 16-bit types,
+// the register-staged one for fp32.
+template <int DT, int QM, int KVM, int RM>
+const void* decode_kernel() {
+    if constexpr (DT == kF32) return reinterpret_cast<const void*>(&dv_decode<DT, QM, KVM, RM>);
+    else return reinterpret_cast<const void*>(&dv_stream<DT, QM, KVM, RM>);
+}
+
+template <int DT>
+size_t wave_lds() {
+    return DT == kF32 ? (size_t)vt_bytes<DT>() : (size_t)stream::kWaveLds;
+}
+
 // Resident workgroups per CU for one kernel instance at a given dynamic LDS
 // size, cached per 1 KiB of LDS (hipOccupancy queries cost host time).
 template <int DT, int QM, int KVM, int RM>
@@ -736,8 +959,8 @@ int resident_wgs(int hpw, size_t lds) {
     int& slot = cache[hpw - 1][kib];
     if (slot == 0) {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(&dv_decode<DT, QM, KVM, RM>),
-                                                         hpw * kWave, (size_t)kib * 1024) != hipSuccess ||
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_kernel<DT, QM, KVM, RM>(), hpw * kWave,
+                                                         (size_t)kib * 1024) != hipSuccess ||
             nb < 1)
             nb = 1;
         slot = nb;
@@ -747,14 +970,14 @@ int resident_wgs(int hpw, size_t lds) {
 
 template <int DT, int QM, int KVM, int RM>
 hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, hipStream_t stream) {
-    const size_t lds = (size_t)p.hpw * vt_bytes<DT>() + (size_t)(p.nrows + 1) * sizeof(long long);
+    const size_t lds = (size_t)p.hpw * wave_lds<DT>() + (size_t)(p.nrows + 1) * sizeof(long long);
+    const void* kern = decode_kernel<DT, QM, KVM, RM>();
     static bool attr_set = false;
     if (!attr_set) {
         // largest dynamic LDS any launch of this kernel asks for (4 waves, kMaxRows rows)
-        const size_t max_lds = (size_t)kMaxWavesPerWg * vt_bytes<DT>() + (size_t)(kMaxRows + 1) * sizeof(long long);
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_decode<DT, QM, KVM, RM>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
-        if (e != hipSuccess) return note_site(e, "hipFuncSetAttribute(dv_decode)");
+        const size_t max_lds = (size_t)kMaxWavesPerWg * wave_lds<DT>() + (size_t)(kMaxRows + 1) * sizeof(long long);
+        hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
+        if (e != hipSuccess) return note_site(e, "hipFuncSetAttribute(decode)");
         attr_set = true;
     }
     // one wave of workgroups that are all resident at once, bounded by the work
@@ -762,9 +985,12 @@ hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, 
     if (nwg > max_wg) nwg = max_wg;
     if (nwg > cap) nwg = cap;
     p.nwg = nwg < 1 ? 1 : (int)nwg;
-    hipLaunchKernelGGL((dv_decode<DT, QM, KVM, RM>), dim3(p.nwg), dim3(p.hpw * kWave), lds, stream, p);
+    if constexpr (DT == kF32)
+        hipLaunchKernelGGL((dv_decode<DT, QM, KVM, RM>), dim3(p.nwg), dim3(p.hpw * kWave), lds, stream, p);
+    else
+        hipLaunchKernelGGL((dv_stream<DT, QM, KVM, RM>), dim3(p.nwg), dim3(p.hpw * kWave), lds, stream, p);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return note_site(e, "launch dv_decode");
+    if (e != hipSuccess) return note_site(e, "launch decode");
     const int nseg = p.nrows * (p.Hkv / p.hpw);
     hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg * p.hpw), dim3(256), 0, stream, p);
     e = hipGetLastError();

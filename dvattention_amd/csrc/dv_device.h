@@ -81,6 +81,29 @@ __device__ inline u32x2 lds_read_tr16(const unsigned char* p) {
 
 __device__ inline void compiler_fence() { asm volatile("" ::: "memory"); }
 
+// ---- direct-to-LDS loads ------------------------------------------------------
+
+__device__ inline uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)(p));
+}
+
+// 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane
+// (global_load_lds_dwordx4).  lds_base must be wave-uniform.  The compiler does
+// not track these loads: completion is awaited with wait_vmcnt.
+__device__ inline void dma16(const void* gptr, uint32_t lds_base) {
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
+                 : "memory", "m0");
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding.
+template <int N>
+__device__ inline void wait_vmcnt() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Wait until this wave's LDS operations are complete.
+__device__ inline void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 // ---- wave-level helpers -----------------------------------------------------
 
 __device__ inline float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
