@@ -13,7 +13,8 @@ in the 256 MB Infinity Cache (cold HBM reads, as in a real multi-layer decode
 step).  Every configuration is also reported under ``per_config``.
 
 ``roofline`` covers the decode kernel family (decode + split-merge launch of one
-call), timed with HIP events on the stream the kernels run on.  ``cpu_baseline``
+call), timed with HIP events on the stream the kernels run on; ``traffic`` is the
+HBM bytes per call measured with rocprofv3 counters (profiles/).  ``cpu_baseline``
 times the CPU oracle (the fp32 restatement of the reference's eager path) on a
 bounded sample of configuration 2, on this host's cores.
 """
@@ -194,6 +195,13 @@ def main() -> int:
             f"kernel {r['kernel_us_mean']} us, {r['achieved_GBs']} GB/s = {100 * r['hbm_frac']:.1f}% HBM, "
             f"{r['achieved_TFLOPs']} TFLOP/s")
     head = per[2]
+    # HBM bytes per call from the committed rocprofv3 --pmc summary (FETCH_SIZE / WRITE_SIZE
+    # scaled by a 1 GiB copy); absent -> null
+    traffic = {}
+    tpath = os.path.join(HERE, "profiles", "dv_stream_cfg2_hbm_traffic.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f)
     copy_gbs = measure_copy(device)
     log(f"[bench] device copy (1 GiB read + 1 GiB write): {copy_gbs:.0f} GB/s")
     cpu = None if args.no_cpu else cpu_baseline(device)
@@ -214,8 +222,9 @@ def main() -> int:
                    "q_heads": 128, "head_dim": 128, "page_size": 16, "kv_len": "U[1024,8192]",
                    "rotary_dim": 128, "replicas": head["replicas"]},
         "roofline": {"bound": "hbm", "achieved": head["achieved_GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": head["hbm_frac"], "traffic": None,
-                     "kernel": "dv_decode + dv_merge (one call)", "alg_bytes_per_launch": head["alg_bytes"],
+                     "frac": head["hbm_frac"], "traffic": traffic.get("traffic_bytes_per_call"),
+                     "traffic_source": traffic.get("source"),
+                     "kernel": "dv_stream + dv_merge (one call)", "alg_bytes_per_launch": head["alg_bytes"],
                      "launch_us": head["kernel_us_mean"], "copy_GBs": round(copy_gbs, 1)},
         "cpu_baseline": cpu,
         "per_config": [per[i] for i in sorted(per)],
