@@ -134,6 +134,7 @@ __device__ inline void tile_softmax_pv(Tile& t, const f32x4& s0, const f32x4& s1
                       pack2<DT>(pr[6], pr[7])};
 #pragma unroll
     for (int c = 0; c < 8; ++c) t.o[c] = Tr<DT>::mma(vA[c], pB, t.o[c] * alpha);
+    mfma_settle(t.o);
 }
 
 // Query tiles of this wave's tokens for view f, staged through LDS (the K/V ring

@@ -675,6 +675,7 @@ __device__ inline void compute(SoftState& st, const unsigned char* kt, const uns
                       pack2<DT>(pr[6], pr[7])};
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc) st.o[cc] = Tr<DT>::mma(vA[cc], pB, st.o[cc]);
+    mfma_settle(st.o);
 }
 
 // One wave: KV head hkv over visible keys [v0, v1) of one row.  wlds: this

@@ -61,6 +61,17 @@ __device__ inline uint32_t pack2(float lo, float hi) {
     return (uint32_t)Tr<DT>::fromf(lo) | ((uint32_t)Tr<DT>::fromf(hi) << 16);
 }
 
+// A VALU read of an MFMA result needs software wait states after the MFMA that
+// wrote it (11-19 for the 8- and 16-pass XDL ops).  The compiler provides them
+// inside a block but was seen to miss them where a branch leads straight to a
+// loop-carried copy of the accumulators (the copy read stale elements).  This
+// barrier depends on all eight accumulators, so it follows the last MFMA that
+// writes them, and puts 24 wait states before any later instruction.
+__device__ inline void mfma_settle(f32x4 (&o)[8]) {
+    asm volatile("s_nop 7\n\ts_nop 7\n\ts_nop 7"
+                 : "+v"(o[0]), "+v"(o[1]), "+v"(o[2]), "+v"(o[3]), "+v"(o[4]), "+v"(o[5]), "+v"(o[6]), "+v"(o[7]));
+}
+
 // ---- memory helpers ---------------------------------------------------------
 
 // 16-byte loads from global memory (address space 1, so the compiler emits
@@ -89,9 +100,12 @@ __device__ inline uint32_t lds_addr(const void* p) {
 
 // 16 bytes per lane from global memory straight into LDS at m0 + 16 * lane
 // (global_load_lds_dwordx4).  lds_base must be wave-uniform.  The compiler does
-// not track these loads: completion is awaited with wait_vmcnt.
+// not track these loads: completion is awaited with wait_vmcnt.  An SALU write of
+// m0 needs one wait state before an LDS-DMA instruction reads it (the compiler's
+// hazard recognizer inserts the same s_nop for its own global_load_lds); without
+// it the first lanes of the load can use the previous m0.
 __device__ inline void dma16(const void* gptr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
                  : "memory", "m0");
 }
 
