@@ -97,44 +97,13 @@ struct Tile {
     float m, l;
 };
 
+// Online softmax of one tile for one 32-key stage (softmax32); returns the P^T
+// MFMA operand.
 template <int DT>
-__device__ inline void tile_softmax_pv(Tile& t, const f32x4& s0, const f32x4& s1, uint32_t mask, float l2scale,
-                                       const u32x4 (&vA)[8]) {
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;
-    float tv[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        tv[i] = ((mask >> (g * 4 + i)) & 1u) ? s0[i] * l2scale : -DV_INF;
-        tv[4 + i] = ((mask >> (16 + g * 4 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
-    }
-    float mx = tv[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, tv[i]);
-    mx = fmaxf(mx, shfl_xor_f(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    const float mnew = fmaxf(t.m, mx);
+__device__ inline u32x4 tile_softmax(Tile& t, const f32x4& s0, const f32x4& s1, uint32_t mask, float l2scale) {
     float pr[8];
-    float alpha;
-    if (mnew == -DV_INF) {
-        alpha = 1.0f;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = 0.0f;
-    } else {
-        alpha = exp2f(t.m - mnew);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = exp2f(tv[i] - mnew);
-    }
-    float ps = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) ps += pr[i];
-    t.l = t.l * alpha + ps;
-    t.m = mnew;
-    const u32x4 pB = {pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]),
-                      pack2<DT>(pr[6], pr[7])};
-#pragma unroll
-    for (int c = 0; c < 8; ++c) t.o[c] = Tr<DT>::mma(vA[c], pB, t.o[c] * alpha);
-    mfma_settle(t.o);
+    softmax32(t.o, t.m, t.l, s0, s1, mask, l2scale, pr);
+    return u32x4{pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]), pack2<DT>(pr[6], pr[7])};
 }
 
 // Query tiles of this wave's tokens for view f, staged through LDS (the K/V ring
@@ -296,7 +265,7 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
         const long long a = v0 > P ? v0 : P;
         const long long bnd = v1 < P + vis_blk ? v1 : P + vis_blk;
         if (a < bnd) {
-            u32x4 qB[kTiles][4];
+            u32x4 qB[kTiles][4] = {};
             // the ring is idle here (previous range drained): stage the query tiles in it
             stage_q_tiles<DT, QM>(p, smem + wv * (kTiles * 4096),
                                   reinterpret_cast<float*>(smem + kWaves * kTiles * 4096 + wv * kTiles * 512), w,
@@ -356,17 +325,35 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                     // visibility of the 32 keys (page validity and range end)
                     const bool kv_ok = row_of<KVM>(p, r, pages, kb0 + (lane & 31)) >= 0;
                     const uint32_t okmask = (uint32_t)ballot(kv_ok && lane < 32);
-                    // K operand: lane (g, m) <- key kb*16+m, dims c*32 + g*8
-                    u32x4 kA[2][4];
+                    // S^T = K Q^T for both tiles: the K operand of each 32-dim slice is
+                    // read once and used by both (tiles past the token count have a zero
+                    // query and no visible key, so they need no branch)
+                    f32x4 s0[kTiles], s1[kTiles];
 #pragma unroll
-                    for (int kb = 0; kb < 2; ++kb)
+                    for (int t = 0; t < kTiles; ++t) {
+                        s0[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                        s1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    }
 #pragma unroll
-                        for (int cc = 0; cc < 4; ++cc) {
-                            const int key = kb * 16 + n;
-                            kA[kb][cc] = *reinterpret_cast<const u32x4*>(kt + key * 256 + swz_k(key, cc * 4 + g) * 16);
+                    for (int cc = 0; cc < 4; ++cc) {
+                        const u32x4 a0 = *reinterpret_cast<const u32x4*>(kt + n * 256 + swz_k(n, cc * 4 + g) * 16);
+                        const u32x4 a1 =
+                            *reinterpret_cast<const u32x4*>(kt + (16 + n) * 256 + swz_k(16 + n, cc * 4 + g) * 16);
+#pragma unroll
+                        for (int t = 0; t < kTiles; ++t) {
+                            s0[t] = Tr<DT>::mma(a0, qB[t][cc], s0[t]);
+                            s1[t] = Tr<DT>::mma(a1, qB[t][cc], s1[t]);
                         }
-                    // V^T operand: block lane sl -> key g*4 + sl/4 (+16), dims c*16 + (sl%4)*4
-                    u32x4 vA[8];
+                    }
+                    u32x4 pB[kTiles];
+#pragma unroll
+                    for (int t = 0; t < kTiles; ++t) {
+                        const int lim = vis_t[t] - kb0;
+                        const uint32_t lm = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
+                        pB[t] = tile_softmax<DT>(tl[t], s0[t], s1[t], okmask & lm, p.l2scale);
+                    }
+                    // O^T += V^T P^T: block lane sl -> key g*4 + sl/4 (+16), dims
+                    // cc*16 + (sl%4)*4; each 16-dim slice of V^T is read once for both tiles
                     {
                         const int sl = lane & 15;
                         const int k0 = g * 4 + (sl >> 2);
@@ -377,23 +364,13 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                             const int piece = cc * 2 + ((sl & 3) >> 1);
                             const u32x2 a0 = lds_read_tr16(vt + k0 * 256 + swz_v(k0, piece) * 16 + hb);
                             const u32x2 a1 = lds_read_tr16(vt + k1 * 256 + swz_v(k1, piece) * 16 + hb);
-                            vA[cc] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                            const u32x4 va = {a0[0], a0[1], a1[0], a1[1]};
+#pragma unroll
+                            for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va, pB[t], tl[t].o[cc]);
                         }
                     }
 #pragma unroll
-                    for (int t = 0; t < kTiles; ++t) {
-                        if (t < ntile) {
-                            f32x4 s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                            for (int cc = 0; cc < 4; ++cc) {
-                                s0 = Tr<DT>::mma(kA[0][cc], qB[t][cc], s0);
-                                s1 = Tr<DT>::mma(kA[1][cc], qB[t][cc], s1);
-                            }
-                            const int lim = vis_t[t] - kb0;
-                            const uint32_t lm = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
-                            tile_softmax_pv<DT>(tl[t], s0, s1, okmask & lm, p.l2scale, vA);
-                        }
-                    }
+                    for (int t = 0; t < kTiles; ++t) mfma_settle(tl[t].o);
                     lds_barrier();  // every wave is done with this stage before it is refilled
                 }
                 wait_vmcnt<0>();    // the trailing zero-row stages land before the ring is reused
@@ -408,8 +385,7 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
         if (t >= ntile) continue;
-        float lt = tl[t].l + shfl_xor_f(tl[t].l, 16);
-        lt += shfl_xor_f(lt, 32);
+        const float lt = rows4_sum(tl[t].l);
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
         const int s = tok0 + t;
         const int h = hkv * kGqa + n;

@@ -171,36 +171,7 @@ struct SoftState {
 // Returns the unnormalised probabilities (8 per lane) in pr.
 __device__ inline void softmax_step(SoftState& st, const f32x4& s0, const f32x4& s1, uint32_t mask,
                                     float l2scale, float (&pr)[8]) {
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;
-    float t[8];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        t[i] = ((mask >> (g * 4 + i)) & 1u) ? s0[i] * l2scale : -DV_INF;
-        t[4 + i] = ((mask >> (16 + g * 4 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
-    }
-    float mx = t[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) mx = fmaxf(mx, t[i]);
-    mx = fmaxf(mx, shfl_xor_f(mx, 16));
-    mx = fmaxf(mx, shfl_xor_f(mx, 32));
-    const float mnew = fmaxf(st.m, mx);
-    // The accumulator is rescaled only when some head's running max grows, which
-    // after the first steps is rare; otherwise alpha == 1 for every lane.
-    if (ballot(mnew > st.m)) {
-        const float alpha = mnew == -DV_INF ? 1.0f : exp2f(st.m - mnew);
-        st.l *= alpha;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) st.o[c] *= alpha;
-        st.m = mnew;
-    }
-    float ps = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        pr[i] = mnew == -DV_INF ? 0.0f : exp2f(t[i] - mnew);
-        ps += pr[i];
-    }
-    st.l += ps;
+    softmax32(st.o, st.m, st.l, s0, s1, mask, l2scale, pr);
 }
 
 // fp32: lane (g, m) loads dims [c*16 + g*4, +4), c = 0..7, of keys m and 16+m.
@@ -403,8 +374,7 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
     }
 
     // epilogue: total over the four lane groups, normalise, base-2 LSE
-    float lt = st.l + shfl_xor_f(st.l, 16);
-    lt += shfl_xor_f(lt, 32);
+    const float lt = rows4_sum(st.l);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int h = hkv * kGqa + n;
     if (final_out) {
@@ -777,8 +747,7 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
     }
 
     // epilogue: total over the four lane groups, normalise, base-2 LSE
-    float lt = st.l + shfl_xor_f(st.l, 16);
-    lt += shfl_xor_f(lt, 32);
+    const float lt = rows4_sum(st.l);
     const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
     const int h = hkv * kGqa + n;
     if (final_out) {

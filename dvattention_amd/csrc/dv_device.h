@@ -56,9 +56,18 @@ template <> struct Tr<kF32> {
     }
 };
 
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+// Two floats rounded to the 16-bit storage type (round to nearest even), lo in
+// bits 0-15: one v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32.
 template <int DT>
 __device__ inline uint32_t pack2(float lo, float hi) {
-    return (uint32_t)Tr<DT>::fromf(lo) | ((uint32_t)Tr<DT>::fromf(hi) << 16);
+    static_assert(DT == kBF16 || DT == kF16, "16-bit storage types only");
+    const f32x2 v = {lo, hi};
+    if constexpr (DT == kBF16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+    else return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, f16x2));
 }
 
 // A VALU read of an MFMA result needs software wait states after the MFMA that
@@ -120,9 +129,85 @@ __device__ inline void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "mem
 
 // ---- wave-level helpers -----------------------------------------------------
 
-__device__ inline float shfl_xor_f(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// Max / sum over the four 16-lane rows of a wave (lanes n, n+16, n+32, n+48),
+// every lane receiving the result, with the gfx950 row-swap permutes (VALU;
+// no LDS round trip).  permlane16_swap(v, v) returns rows (0,0,2,2) and (1,1,3,3)
+// of v, permlane32_swap(v, v) rows (0,1,0,1) and (2,3,2,3); the sum is formed as
+// (r0 + r1) + (r2 + r3) in every lane.
+__device__ inline float rows4_max(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ inline float rows4_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 __device__ inline int shfl_i(int v, int src) { return __shfl(v, src, kWave); }
 __device__ inline uint64_t ballot(bool b) { return __ballot(b); }
+
+// ---- online softmax ---------------------------------------------------------
+
+// The running max is raised only when a row's new max exceeds it by more than
+// this many base-2 units; below that, probabilities exp2(x - m) may reach 2^8,
+// which fp32 accumulators and the 16-bit P operand hold with the same relative
+// precision as values below 1.  The result is mathematically the same softmax.
+constexpr float kMaxSlack = 8.0f;
+
+// One online-softmax step over a 32-key stage for the rows of a lane column.
+// s0 / s1: raw scores of keys 0-15 / 16-31 (lane (g, n) holds keys g*4 + i of
+// row n); mask: visible keys (bit k = key k); l2scale: softmax scale / ln 2
+// (p = exp2(score * l2scale - m)).  Updates the running max m, sum l and the
+// accumulators o (rescaled when m is raised); returns the unnormalised p of the
+// lane's 8 keys (keys g*4 + i, then 16 + g*4 + i).
+__device__ inline void softmax32(f32x4 (&o)[8], float& m, float& l, const f32x4& s0, const f32x4& s1,
+                                 uint32_t mask, float l2scale, float (&pr)[8]) {
+    const int g = (threadIdx.x & 63) >> 4;
+    float x[8];
+    bool raw;  // x holds raw scores (scaled in the exponent) rather than scaled ones
+    float mx;
+    if (mask == 0xffffffffu && l2scale > 0.0f) {
+        // every key visible, positive scale: max of the raw scores, scaled once
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[i] = s0[i];
+            x[4 + i] = s1[i];
+        }
+        raw = true;
+        mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+        mx = rows4_max(mx) * l2scale;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            x[i] = ((mask >> (g * 4 + i)) & 1u) ? s0[i] * l2scale : -DV_INF;
+            x[4 + i] = ((mask >> (16 + g * 4 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
+        }
+        raw = false;
+        mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+        mx = rows4_max(mx);
+    }
+    if (ballot(mx > m + kMaxSlack)) {
+        const float mnew = fmaxf(m, mx);
+        const float alpha = mnew == -DV_INF ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
+        l *= alpha;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) o[c] *= alpha;
+        m = mnew;
+    }
+    // m == -inf only while no key of the row has been visible: p = 0
+    const float mm = m == -DV_INF ? 0.0f : m;
+    float ps = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        pr[i] = __builtin_amdgcn_exp2f(raw ? __builtin_fmaf(x[i], l2scale, -mm) : x[i] - mm);
+        ps += pr[i];
+    }
+    l += ps;
+}
 
 // ---- query rotation ---------------------------------------------------------
 // Rotated value of the run of N consecutive dims [d0, d0+N) of one query row,
