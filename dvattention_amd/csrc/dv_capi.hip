@@ -70,6 +70,10 @@ dvattn_status check_pages(const dvattn_shape* s) {
     if (s->block_size <= 0) return fail(DVATTN_ERR_INVALID, "block_size must be positive (got %d)", s->block_size);
     if (s->max_blocks_per_seq < 0 || s->num_blocks < 0)
         return fail(DVATTN_ERR_INVALID, "max_blocks_per_seq / num_blocks must be >= 0");
+    // the kernels index cache rows (block, slot, KV head) with 32-bit integers
+    if ((long long)s->num_blocks * s->block_size * (s->Hkv > 0 ? s->Hkv : 1) >= (1ll << 32))
+        return fail(DVATTN_ERR_UNSUPPORTED, "K/V cache of %lld rows exceeds 2^32 rows",
+                    (long long)s->num_blocks * s->block_size * s->Hkv);
     return DVATTN_OK;
 }
 

@@ -52,25 +52,33 @@ struct Range {
     long long off;           // paged: logical position of the view's key 0
     long long bstride;       // contig: element offset of the sequence's batch entry
     int L;                   // contig: tokens in the fragment tensor
-    long long lp0;           // paged: first cached logical page
+    uint32_t lp0;            // paged: first cached logical page
+    bool pages_ok;           // paged: every page of the current sub-range is valid
     int w, hkv;
     int b;                   // end (exclusive) of the view-local key range
 };
 
-// Element offset of key l's row, or -1 when not visible / not addressable.
+// Byte offset of key l's K (= V) row, or -1 when not visible / not addressable.
+// Paged rows are indexed in 32 bits (the C ABI rejects caches of 2^32 rows or
+// more) and positions are 32-bit as in the reference (paged_kernel_v21.cuh:103-104).
 template <int KVM>
 __device__ inline long long row_of(const DecodeParams& p, const Range& r, const int* pages, int l) {
     if (KVM == kKvPaged) {
-        const long long pos = r.off + l;
-        long long lp;
-        if (p.bs_shift >= 0) lp = pos >> p.bs_shift;
-        else lp = pos >= 0 ? pos / p.bs : -((-pos + p.bs - 1) / p.bs);
-        const long long idx = lp - r.lp0;
-        const int page = (l < r.b && idx >= 0 && idx < kPageCap) ? pages[idx] : -1;
-        const long long rr = pos - lp * p.bs;
-        return page >= 0 ? (((long long)page * p.bs + rr) * p.Hkv + r.hkv) * kHeadDim : -1;
+        const uint32_t pos = (uint32_t)(r.off + l);
+        uint32_t lp, rr;
+        if (p.bs_shift >= 0) {
+            lp = pos >> p.bs_shift;
+            rr = pos & ((1u << p.bs_shift) - 1u);
+        } else {
+            lp = pos / (uint32_t)p.bs;
+            rr = pos - lp * (uint32_t)p.bs;
+        }
+        const uint32_t idx = lp - r.lp0;
+        const int page = (l < r.b && idx < (uint32_t)kPageCap) ? pages[idx] : -1;
+        const uint32_t rowidx = ((uint32_t)page * (uint32_t)p.bs + rr) * (uint32_t)p.Hkv + (uint32_t)r.hkv;
+        return page >= 0 ? (long long)((unsigned long long)rowidx << 8) : -1;
     } else {
-        return l < r.b ? r.bstride + ((long long)r.hkv * r.L + l) * kHeadDim : -1;
+        return l < r.b ? (r.bstride + ((long long)r.hkv * r.L + l) * kHeadDim) * 2 : -1;
     }
 }
 
@@ -85,8 +93,8 @@ __device__ inline void issue_stage(const DecodeParams& p, const Range& r, const 
     const int kl = wv * 4 + (lane >> 4);
     const long long row = row_of<KVM>(p, r, pages, kb0 + kl);
     const int gk = swz_k(kl, pos), gv = swz_v(kl, pos);
-    const unsigned char* ka = row >= 0 ? r.k + (row + gk * 8) * 2 : zrow + gk * 16;
-    const unsigned char* va = row >= 0 ? r.v + (row + gv * 8) * 2 : zrow + gv * 16;
+    const unsigned char* ka = row >= 0 ? r.k + row + gk * 16 : zrow + gk * 16;
+    const unsigned char* va = row >= 0 ? r.v + row + gv * 16 : zrow + gv * 16;
     const uint32_t koff = (uint32_t)(wv * 4) * 256;
     dma16(ka, __builtin_amdgcn_readfirstlane(sbase + koff));
     dma16(va, __builtin_amdgcn_readfirstlane(sbase + kKvBytes + koff));
@@ -295,21 +303,24 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
             for (int sa = la; sa < lb; sa += span) {
                 const int sbnd = sa + span < lb ? sa + span : lb;
                 r.b = sbnd;
+                r.pages_ok = true;
                 if (KVM == kKvPaged) {
-                    const long long p0 = off + sa;
-                    r.lp0 = p.bs_shift >= 0 ? (p0 >> p.bs_shift)
-                                            : (p0 >= 0 ? p0 / p.bs : -((-p0 + p.bs - 1) / p.bs));
+                    const uint32_t p0 = (uint32_t)(off + sa), p1 = (uint32_t)(off + sbnd - 1);
+                    const uint32_t lpl = p.bs_shift >= 0 ? (p1 >> p.bs_shift) : p1 / (uint32_t)p.bs;
+                    r.lp0 = p.bs_shift >= 0 ? (p0 >> p.bs_shift) : p0 / (uint32_t)p.bs;
                     __syncthreads();
+                    bool ok = true;  // every page this thread loaded for the sub-range is valid
                     for (int i = tid; i < kPageCap; i += blockDim.x) {
-                        const long long lp = r.lp0 + i;
+                        const uint32_t lp = r.lp0 + (uint32_t)i;
                         int pg = -1;
-                        if (lp >= 0 && lp < p.maxB) {
+                        if (lp < (uint32_t)p.maxB) {
                             pg = p.bt[(long long)w * p.maxB + lp];
                             if (pg < 0 || pg >= p.nblocks) pg = -1;
                         }
                         pages[i] = pg;
+                        if (lp <= lpl && pg < 0) ok = false;
                     }
-                    __syncthreads();
+                    r.pages_ok = __syncthreads_and(ok) != 0;
                 }
                 const int nsteps = (sbnd - sa + kStep - 1) / kStep;
                 // prologue: stages 0 .. kStages-2 (past the end: rows of zeros)
@@ -322,9 +333,16 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                     const int kb0 = sa + i * kStep;
                     const unsigned char* kt = smem + (i % kStages) * kStageBytes;
                     const unsigned char* vt = kt + kKvBytes;
-                    // visibility of the 32 keys (page validity and range end)
-                    const bool kv_ok = row_of<KVM>(p, r, pages, kb0 + (lane & 31)) >= 0;
-                    const uint32_t okmask = (uint32_t)ballot(kv_ok && lane < 32);
+                    // visibility of the 32 keys: the range end, and page validity when
+                    // some page of the sub-range is missing
+                    uint32_t okmask;
+                    if (r.pages_ok) {
+                        const int nin = sbnd - kb0;
+                        okmask = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
+                    } else {
+                        const bool kv_ok = row_of<KVM>(p, r, pages, kb0 + (lane & 31)) >= 0;
+                        okmask = (uint32_t)ballot(kv_ok && lane < 32);
+                    }
                     // S^T = K Q^T for both tiles: the K operand of each 32-dim slice is
                     // read once and used by both (tiles past the token count have a zero
                     // query and no visible key, so they need no branch)
@@ -334,11 +352,13 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                         s0[t] = f32x4{0.f, 0.f, 0.f, 0.f};
                         s1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
                     }
+                    // K row n (and 16 + n), piece (cc*4 + g) ^ n: the swizzle only flips
+                    // address bits 6-7 of kbase, so slice cc is at kbase ^ (64 cc)
+                    const uint32_t kbase = lds_addr(kt) + (uint32_t)(n * 256 + 16 * (g ^ (n & 3)) + 64 * (n >> 2));
 #pragma unroll
                     for (int cc = 0; cc < 4; ++cc) {
-                        const u32x4 a0 = *reinterpret_cast<const u32x4*>(kt + n * 256 + swz_k(n, cc * 4 + g) * 16);
-                        const u32x4 a1 =
-                            *reinterpret_cast<const u32x4*>(kt + (16 + n) * 256 + swz_k(16 + n, cc * 4 + g) * 16);
+                        const u32x4 a0 = lds_read16_at(kbase ^ (uint32_t)(64 * cc));
+                        const u32x4 a1 = lds_read16_at((kbase ^ (uint32_t)(64 * cc)) + 16 * 256);
 #pragma unroll
                         for (int t = 0; t < kTiles; ++t) {
                             s0[t] = Tr<DT>::mma(a0, qB[t][cc], s0[t]);
@@ -355,15 +375,17 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                     // O^T += V^T P^T: block lane sl -> key g*4 + sl/4 (+16), dims
                     // cc*16 + (sl%4)*4; each 16-dim slice of V^T is read once for both tiles
                     {
+                        // row k0 (and k0 + 16), piece (cc*2 + b) ^ ((k0 & 7) << 1), byte hb:
+                        // the swizzle only flips address bits 5-7 of vbase, so slice cc is
+                        // at vbase ^ (32 cc)
                         const int sl = lane & 15;
                         const int k0 = g * 4 + (sl >> 2);
-                        const int k1 = k0 + 16;
-                        const int hb = (sl & 1) * 8;
+                        const uint32_t vbase = lds_addr(vt) + (uint32_t)(k0 * 256 + 16 * ((sl & 3) >> 1) +
+                                                                         (sl & 1) * 8 + 32 * (k0 & 7));
 #pragma unroll
                         for (int cc = 0; cc < 8; ++cc) {
-                            const int piece = cc * 2 + ((sl & 3) >> 1);
-                            const u32x2 a0 = lds_read_tr16(vt + k0 * 256 + swz_v(k0, piece) * 16 + hb);
-                            const u32x2 a1 = lds_read_tr16(vt + k1 * 256 + swz_v(k1, piece) * 16 + hb);
+                            const u32x2 a0 = lds_read_tr16_at(vbase ^ (uint32_t)(32 * cc));
+                            const u32x2 a1 = lds_read_tr16_at((vbase ^ (uint32_t)(32 * cc)) + 16 * 256);
                             const u32x4 va = {a0[0], a0[1], a1[0], a1[1]};
 #pragma unroll
                             for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va, pB[t], tl[t].o[cc]);
@@ -411,12 +433,15 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
 
 template <int DT, int QM, int KVM>
 __global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
-    extern __shared__ __align__(16) unsigned char smem[];
-    __shared__ long long s_scan[kWaves];
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    // the ring starts at a 256-byte aligned LDS address (the XOR addressing of
+    // the MFMA operands needs address bits 0-7 of every tile base clear)
+    unsigned char* smem = smem_raw + ((256u - (lds_addr(smem_raw) & 255u)) & 255u);
     const int tid = threadIdx.x;
     const int wv = tid >> 6, lane = tid & 63;
     int* pages = reinterpret_cast<int*>(smem + kRingBytes);
-    long long* s_pref = reinterpret_cast<long long*>(smem + kRingBytes + kPageCap * 4);
+    long long* s_scan = reinterpret_cast<long long*>(smem + kRingBytes + kPageCap * 4);  // kWaves entries
+    long long* s_pref = s_scan + kWaves;
     const int NHG = p.Hkv;  // one KV head per workgroup
 
     // 1. visible keys per row group -> exclusive prefix sums
@@ -563,7 +588,7 @@ __global__ __launch_bounds__(256) void dv_merge_chunk(const DecodeParams p) {
 }
 
 size_t lds_bytes(int nrows) {
-    return (size_t)kRingBytes + (size_t)kPageCap * 4 + (size_t)(nrows + 1) * sizeof(long long);
+    return 256 + (size_t)kRingBytes + (size_t)kPageCap * 4 + (size_t)(kWaves + nrows + 1) * sizeof(long long);
 }
 
 template <int DT, int QM, int KVM>

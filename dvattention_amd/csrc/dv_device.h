@@ -99,6 +99,18 @@ __device__ inline u32x2 lds_read_tr16(const unsigned char* p) {
     return __builtin_bit_cast(u32x2, v);
 }
 
+// The same at an LDS byte address (lets the compiler fold constant offsets into
+// the instruction).
+__device__ inline u32x2 lds_read_tr16_at(uint32_t addr) {
+    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(uintptr_t)addr);
+    return __builtin_bit_cast(u32x2, v);
+}
+__device__ inline u32x4 lds_read16_at(uint32_t addr) {
+    typedef __attribute__((address_space(3))) const u32x4 lds_u32x4;
+    return *(lds_u32x4*)(uintptr_t)addr;
+}
+
 __device__ inline void compiler_fence() { asm volatile("" ::: "memory"); }
 
 // ---- direct-to-LDS loads ------------------------------------------------------
@@ -167,45 +179,44 @@ constexpr float kMaxSlack = 8.0f;
 __device__ inline void softmax32(f32x4 (&o)[8], float& m, float& l, const f32x4& s0, const f32x4& s1,
                                  uint32_t mask, float l2scale, float (&pr)[8]) {
     const int g = (threadIdx.x & 63) >> 4;
-    float x[8];
-    bool raw;  // x holds raw scores (scaled in the exponent) rather than scaled ones
-    float mx;
+    // raise the running max (rescaling the accumulators) if some row needs it;
+    // returns the max to subtract (0 while the row has no visible key: p = 0)
+    auto update = [&](float mx) -> float {
+        if (ballot(mx > m + kMaxSlack)) {
+            const float mnew = fmaxf(m, mx);
+            const float alpha = mnew == -DV_INF ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
+            l *= alpha;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) o[c] *= alpha;
+            m = mnew;
+        }
+        return m == -DV_INF ? 0.0f : m;
+    };
+    float ps = 0.0f;
     if (mask == 0xffffffffu && l2scale > 0.0f) {
-        // every key visible, positive scale: max of the raw scores, scaled once
+        // every key visible, positive scale: max of the raw scores, scaled once,
+        // and p = exp2(s * l2scale - m) in one fma
+        float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+        const float nm = -update(rows4_max(mx) * l2scale);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            x[i] = s0[i];
-            x[4 + i] = s1[i];
+            pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], l2scale, nm));
+            pr[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], l2scale, nm));
         }
-        raw = true;
-        mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-        mx = rows4_max(mx) * l2scale;
     } else {
+        float x[8];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             x[i] = ((mask >> (g * 4 + i)) & 1u) ? s0[i] * l2scale : -DV_INF;
             x[4 + i] = ((mask >> (16 + g * 4 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
         }
-        raw = false;
-        mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-        mx = rows4_max(mx);
-    }
-    if (ballot(mx > m + kMaxSlack)) {
-        const float mnew = fmaxf(m, mx);
-        const float alpha = mnew == -DV_INF ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
-        l *= alpha;
+        float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
+        const float mm = update(rows4_max(mx));
 #pragma unroll
-        for (int c = 0; c < 8; ++c) o[c] *= alpha;
-        m = mnew;
+        for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - mm);
     }
-    // m == -inf only while no key of the row has been visible: p = 0
-    const float mm = m == -DV_INF ? 0.0f : m;
-    float ps = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        pr[i] = __builtin_amdgcn_exp2f(raw ? __builtin_fmaf(x[i], l2scale, -mm) : x[i] - mm);
-        ps += pr[i];
-    }
+    for (int i = 0; i < 8; ++i) ps += pr[i];
     l += ps;
 }
 
