@@ -73,10 +73,13 @@ __device__ inline long long row_of(const DecodeParams& p, const Range& r, const 
             lp = pos / (uint32_t)p.bs;
             rr = pos - lp * (uint32_t)p.bs;
         }
+        // the page-cache read is unconditional (clamped index), so no branch
+        // forms around it
         const uint32_t idx = lp - r.lp0;
-        const int page = (l < r.b && idx < (uint32_t)kPageCap) ? pages[idx] : -1;
-        const uint32_t rowidx = ((uint32_t)page * (uint32_t)p.bs + rr) * (uint32_t)p.Hkv + (uint32_t)r.hkv;
-        return page >= 0 ? (long long)((unsigned long long)rowidx << 8) : -1;
+        const int pg = pages[idx < (uint32_t)kPageCap ? idx : (uint32_t)(kPageCap - 1)];
+        const bool ok = l < r.b && idx < (uint32_t)kPageCap && pg >= 0;
+        const uint32_t rowidx = ((uint32_t)pg * (uint32_t)p.bs + rr) * (uint32_t)p.Hkv + (uint32_t)r.hkv;
+        return ok ? (long long)((unsigned long long)rowidx << 8) : -1;
     } else {
         return l < r.b ? (r.bstride + ((long long)r.hkv * r.L + l) * kHeadDim) * 2 : -1;
     }
