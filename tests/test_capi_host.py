@@ -75,6 +75,8 @@ def _paged(shape, dtype=2, out=1, ws_bytes=1 << 30):
     (dict(rotary_dim=130), 2, "rotary_dim"),
     (dict(block_size=0), 1, "block_size"),
     (dict(F=-1), 1, "negative"),
+    # cache rows (block, slot, KV head) are indexed in 32 bits by the kernels
+    (dict(num_blocks=1 << 28, block_size=16, Hkv=1, Hq=16), 2, "2^32 rows"),
 ])
 def test_paged_rejects_unsupported_shapes(kw, status, needle):
     from dvattention_amd import capi
