@@ -64,8 +64,18 @@ __device__ inline int view_vis(const DecodeParams& p, int f, int locv) {
 
 template <int KVM, int RM>
 __device__ inline long long row_visible(const DecodeParams& p, int row) {
+    // views four at a time, their loads issued together (one memory round trip
+    // per four views instead of two per view)
     long long v = 0;
-    for (int f = 0; f < p.F; ++f) v += view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
+    int f = 0;
+    for (; f + 4 <= p.F; f += 4) {
+        int lc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) lc[j] = row_loc<RM>(p, row, f + j);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v += view_vis<KVM>(p, f + j, lc[j]);
+    }
+    for (; f < p.F; ++f) v += view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
     return v;
 }
 
@@ -430,7 +440,11 @@ __device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, lo
     const int r0 = tid * per;
     const int r1 = r0 + per < nrows ? r0 + per : nrows;
     long long mine = 0;
-    for (int r = r0; r < r1; ++r) mine += row_visible<KVM, RM>(p, p.row_begin + r);
+    for (int r = r0; r < r1; ++r) {
+        const long long v = row_visible<KVM, RM>(p, p.row_begin + r);
+        s_pref[r] = v;  // the row's count, replaced by its prefix below
+        mine += v;
+    }
     const int lane = tid & 63;
     long long incl = mine;
 #pragma unroll
@@ -444,8 +458,9 @@ __device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, lo
     for (int i = 0; i < wv; ++i) before += s_scan[i];
     long long run = before + incl - mine;
     for (int r = r0; r < r1; ++r) {
+        const long long v = s_pref[r];
         s_pref[r] = run;
-        run += row_visible<KVM, RM>(p, p.row_begin + r);
+        run += v;
     }
     long long total = 0;
     for (int i = 0; i < nthreads / kWave; ++i) total += s_scan[i];
