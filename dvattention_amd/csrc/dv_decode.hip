@@ -79,6 +79,60 @@ __device__ inline long long row_visible(const DecodeParams& p, int row) {
     return v;
 }
 
+// The views of one query row, view f in lane f (F <= 64), from one round of
+// loads: visible keys, visible keys of the earlier views, and logical position
+// of the view's key 0 (sum of the earlier fragment_lengths).
+struct ViewTab {
+    int vis;
+    long long P, off;
+};
+
+template <int KVM, int RM>
+__device__ inline ViewTab view_table(const DecodeParams& p, int row) {
+    const int lane = threadIdx.x & 63;
+    int vis = 0;
+    long long fl = 0;
+    if (lane < p.F) {
+        vis = view_vis<KVM>(p, lane, row_loc<RM>(p, row, lane));
+        fl = p.fl[lane];
+    }
+    long long sv = vis, so = fl;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const long long tv = __shfl_up(sv, d, kWave);
+        const long long to = __shfl_up(so, d, kWave);
+        if (lane >= d) {
+            sv += tv;
+            so += to;
+        }
+    }
+    return ViewTab{vis, sv - vis, so - fl};
+}
+
+// Calls body(f, vis, P, off) for every view of `row` with visible keys in the
+// row's visible-key range [v0, v1), in view order.
+template <int KVM, int RM, class Body>
+__device__ inline void for_views(const DecodeParams& p, int row, long long v0, long long v1, Body&& body) {
+    if (p.F <= kWave) {
+        const int lane = threadIdx.x & 63;
+        const ViewTab t = view_table<KVM, RM>(p, row);
+        uint64_t m = ballot(lane < p.F && t.vis > 0 && t.P < v1 && t.P + t.vis > v0);
+        while (m) {
+            const int f = __builtin_ctzll(m);
+            m &= m - 1;
+            body(f, __shfl(t.vis, f, kWave), __shfl(t.P, f, kWave), __shfl(t.off, f, kWave));
+        }
+        return;
+    }
+    long long P = 0, off = 0;
+    for (int f = 0; f < p.F && P < v1; ++f) {
+        const int vis = view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
+        if (vis > 0 && P + vis > v0) body(f, vis, P, off);
+        P += vis;
+        off += p.fl[f];
+    }
+}
+
 // Sequence of packed token t: first i with t < cu_seqlens_q[i+1], else 0
 // (varlen_paged_kernel_v21.cuh:40-47).  Wave-cooperative, 64 entries per ballot.
 __device__ inline int varlen_seq(const DecodeParams& p, int t) {
@@ -344,13 +398,12 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
     win.wbase = -(1ll << 60);
     win.pg = -1;
 
-    long long P = 0;    // visible keys of the earlier views
-    long long off = 0;  // logical position of view f (paged): sum of earlier fragment_lengths
-    for (int f = 0; f < p.F && P < v1; ++f) {
-        const int vis = view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
+    // P: visible keys of the earlier views; off: logical position of view f
+    // (paged): sum of the earlier fragment_lengths
+    for_views<KVM, RM>(p, row, v0, v1, [&](int f, int vis, long long P, long long off) {
         const long long a = v0 > P ? v0 : P;
         const long long bnd = v1 < P + vis ? v1 : P + vis;
-        if (a < bnd) {
+        {
             const int l0 = (int)(a - P), l1 = (int)(bnd - P);
             KvCtx c;
             c.w = w;
@@ -379,9 +432,7 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
                 compute32(st, b, qB, vt, p.l2scale);
             }
         }
-        P += vis;
-        off += p.fl[f];
-    }
+    });
 
     // epilogue: total over the four lane groups, normalise, base-2 LSE
     const float lt = rows4_sum(st.l);
@@ -683,13 +734,12 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
     st.m = -DV_INF;
     st.l = 0.0f;
 
-    long long P = 0;    // visible keys of the earlier views
-    long long off = 0;  // logical position of view f (paged): sum of earlier fragment_lengths
-    for (int f = 0; f < p.F && P < v1; ++f) {
-        const int vis = view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
+    // P: visible keys of the earlier views; off: logical position of view f
+    // (paged): sum of the earlier fragment_lengths
+    for_views<KVM, RM>(p, row, v0, v1, [&](int f, int vis, long long P, long long off) {
         const long long a = v0 > P ? v0 : P;
         const long long bnd = v1 < P + vis ? v1 : P + vis;
-        if (a < bnd) {
+        {
             const int l0 = (int)(a - P), l1 = (int)(bnd - P);
             View v;
             v.hkv = hkv;
@@ -757,9 +807,7 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
                 sa = sb;
             }
         }
-        P += vis;
-        off += p.fl[f];
-    }
+    });
 
     // epilogue: total over the four lane groups, normalise, base-2 LSE
     const float lt = rows4_sum(st.l);
