@@ -69,6 +69,7 @@ struct DecodeParams {
     int hpw;              // KV heads (waves) per workgroup
     int nwg;              // workgroups launched
     int min_keys;         // smallest key range worth a workgroup
+    int piece_cost;       // fixed cost of starting a segment, in keys (charged in the work split)
     int slot_floats;      // floats per partial slot
     FragDesc frags[kMaxFragArgs];
 };

@@ -471,12 +471,15 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
 
 // ---- work schedule ----------------------------------------------------------------
 
-// Every workgroup computes the same schedule from locations / fragment_lengths:
-// per-row visible key counts -> exclusive prefix sums in LDS (s_pref, nrows + 1
-// entries); all (row, KV-head-group) segments of visible keys laid end to end and
-// cut into equal contiguous chunks, one per workgroup.  Workgroup 0 also writes
+// Every workgroup computes the same schedule from locations / fragment_lengths.
+// The (row, KV-head-group) segments of visible keys are laid end to end, each
+// non-empty one preceded by p.piece_cost keys of "start cost" (the pipeline
+// start of a piece: page ids, query rotation, first loads), and this cost space
+// is cut into equal contiguous chunks, one per workgroup; a workgroup whose
+// chunk crosses into a new segment thus gets fewer real keys.  Per-row cost
+// prefix sums live in LDS (s_pref, nrows + 1 entries).  Workgroup 0 also writes
 // the merge directory (segment -> first partial slot, piece count).  Then
-// piece(row, head_group, v0, v1, final, slot) runs for each segment piece of this
+// piece(row, head_group, v0, v1, final, slot) runs for each piece of this
 // workgroup's chunk; `final` means the segment has no other piece.
 template <int KVM, int RM, class PieceFn>
 __device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, long long* s_scan, PieceFn&& piece) {
@@ -484,8 +487,10 @@ __device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, lo
     const int wv = tid >> 6;
     const int nthreads = blockDim.x;
     const int NHG = p.Hkv / p.hpw;
+    const long long c = p.piece_cost;
 
-    // 1. per-row visible key counts -> exclusive prefix sums in LDS
+    // 1. per-row cost (visible keys + start cost, 0 for an empty row) -> exclusive
+    //    prefix sums in LDS
     const int nrows = p.nrows;
     const int per = (nrows + nthreads - 1) / nthreads;
     const int r0 = tid * per;
@@ -493,8 +498,9 @@ __device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, lo
     long long mine = 0;
     for (int r = r0; r < r1; ++r) {
         const long long v = row_visible<KVM, RM>(p, p.row_begin + r);
-        s_pref[r] = v;  // the row's count, replaced by its prefix below
-        mine += v;
+        const long long d = v > 0 ? v + c : 0;
+        s_pref[r] = d;  // the row's cost, replaced by its prefix below
+        mine += d;
     }
     const int lane = tid & 63;
     long long incl = mine;
@@ -509,30 +515,31 @@ __device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, lo
     for (int i = 0; i < wv; ++i) before += s_scan[i];
     long long run = before + incl - mine;
     for (int r = r0; r < r1; ++r) {
-        const long long v = s_pref[r];
+        const long long d = s_pref[r];
         s_pref[r] = run;
-        run += v;
+        run += d;
     }
     long long total = 0;
     for (int i = 0; i < nthreads / kWave; ++i) total += s_scan[i];
     if (tid == 0) s_pref[nrows] = total;
     __syncthreads();
 
-    // 2. equal chunks of the (row, head-group) key segments laid end to end
-    const long long Wk = total * NHG;
-    const int geff = Wk == 0 ? 0
-                             : (int)((Wk + p.min_keys - 1) / p.min_keys < p.nwg ? (Wk + p.min_keys - 1) / p.min_keys
+    // 2. equal chunks of the cost space; segment (r, hg) spans D_r cost units at
+    //    NHG*pref[r] + hg*D_r, its keys the last D_r - c of them
+    const long long Wc = total * NHG;
+    const int geff = Wc == 0 ? 0
+                             : (int)((Wc + p.min_keys - 1) / p.min_keys < p.nwg ? (Wc + p.min_keys - 1) / p.min_keys
                                                                                 : p.nwg);
-    const long long chunk = geff ? (Wk + geff - 1) / geff : 1;
+    const long long chunk = geff ? (Wc + geff - 1) / geff : 1;
 
     if (blockIdx.x == 0) {
         for (int sg = tid; sg < nrows * NHG; sg += nthreads) {
             const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
-            const long long V = s_pref[r + 1] - s_pref[r];
+            const long long D = s_pref[r + 1] - s_pref[r];
             int base = 0, cnt = 0;
-            if (V > 0) {
-                const long long stt = NHG * s_pref[r] + hg * V;
-                const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
+            if (D > 0) {
+                const long long segc = NHG * s_pref[r] + hg * D;
+                const long long gf = (segc + c) / chunk, gl = (segc + D - 1) / chunk;
                 cnt = (int)(gl - gf + 1);
                 base = (int)gf + sg;
             }
@@ -544,7 +551,7 @@ __device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, lo
     if (gidx >= geff) return;
 
     long long u = gidx * chunk;
-    const long long uend = u + chunk < Wk ? u + chunk : Wk;
+    const long long uend = u + chunk < Wc ? u + chunk : Wc;
     // last row r with NHG*pref[r] <= u
     int lo = 0, hi = nrows - 1;
     while (lo < hi) {
@@ -555,23 +562,24 @@ __device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, lo
     int r = lo;
     while (u < uend && r < nrows) {
         const long long rs = NHG * s_pref[r];
-        const long long V = s_pref[r + 1] - s_pref[r];
-        if (V == 0 || u >= rs + NHG * V) {
+        const long long D = s_pref[r + 1] - s_pref[r];
+        if (D == 0 || u >= rs + NHG * D) {
             ++r;
             continue;
         }
-        const long long rel = u - rs;
-        const int hg = (int)(rel / V);
-        const long long v0 = rel - hg * V;
-        const long long segend = (long long)(hg + 1) * V;
-        const long long lim = (uend - rs < segend ? uend - rs : segend) - (long long)hg * V;
-        const int sg = r * NHG + hg;
-        const long long stt = rs + hg * V;
-        const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
-        const int cnt = (int)(gl - gf + 1);
-        const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
-        piece(p.row_begin + r, hg, v0, lim, cnt == 1, slot);
-        u = stt + lim;
+        const int hg = (int)((u - rs) / D);
+        const long long segc = rs + hg * D;  // the segment's cost range [segc, segc + D)
+        const long long ka = segc + c;       // its keys: cost positions [ka, segc + D)
+        const long long a = u > ka ? u : ka;
+        const long long b = uend < segc + D ? uend : segc + D;
+        if (a < b) {
+            const int sg = r * NHG + hg;
+            const long long gf = ka / chunk, gl = (segc + D - 1) / chunk;
+            const int cnt = (int)(gl - gf + 1);
+            const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
+            piece(p.row_begin + r, hg, a - ka, b - ka, cnt == 1, slot);
+        }
+        u = segc + D;
     }
 }
 
@@ -966,6 +974,10 @@ int pick_hpw(int Hkv) {
     return 1;
 }
 
+// Start cost of a piece in the 16-bit decode's work split, in keys: about the
+// time a workgroup needs to restart its pipeline on a new segment.
+constexpr int kPieceCost = 128;
+
 // workgroups per CU such that about eight waves share a CU
 int wgs_per_cu(int hpw) { return 8 / hpw; }
 
@@ -1083,6 +1095,7 @@ hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const De
     if (ws_bytes < part_bytes + (size_t)rows_cap * nhg * 2 * 4) return hipErrorInvalidValue;
     p.part = reinterpret_cast<float*>(workspace);
     p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
+    p.piece_cost = dtype == kF32 ? 0 : kPieceCost;
     for (int r0 = 0; r0 < nrows_total; r0 += kMaxRows) {
         p.row_begin = r0;
         p.nrows = nrows_total - r0 < kMaxRows ? nrows_total - r0 : kMaxRows;
