@@ -23,6 +23,7 @@
 //    workgroup, fp32 partial slots, dv_merge_chunk).
 #include "dv_common.h"
 #include "dv_device.h"
+#include "dv_schedule.h"
 
 namespace dv {
 namespace chunk {
@@ -37,6 +38,10 @@ constexpr int kStageBytes = 2 * kKvBytes;     // K tile then V tile
 constexpr int kRingBytes = kStages * kStageBytes;
 constexpr int kPageCap = 2048;                // page ids cached in LDS per view sub-range
 constexpr int kDmaPerStage = 2;               // per wave: 1 x K + 1 x V (1 KiB = 4 key rows each)
+
+// Start cost of a piece in the work split, in keys (query staging and rotation,
+// page ids, the ring prologue).
+constexpr int kPieceCost = 256;
 
 static __device__ __align__(16) unsigned char zrow[512];
 
@@ -440,89 +445,15 @@ __global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
     // the ring starts at a 256-byte aligned LDS address (the XOR addressing of
     // the MFMA operands needs address bits 0-7 of every tile base clear)
     unsigned char* smem = smem_raw + ((256u - (lds_addr(smem_raw) & 255u)) & 255u);
-    const int tid = threadIdx.x;
-    const int wv = tid >> 6, lane = tid & 63;
     int* pages = reinterpret_cast<int*>(smem + kRingBytes);
     long long* s_scan = reinterpret_cast<long long*>(smem + kRingBytes + kPageCap * 4);  // kWaves entries
     long long* s_pref = s_scan + kWaves;
     const int NHG = p.Hkv;  // one KV head per workgroup
 
-    // 1. visible keys per row group -> exclusive prefix sums
-    const int nrows = p.nrows;
-    const int per = (nrows + kThreads - 1) / kThreads;
-    const int r0 = tid * per;
-    const int r1 = r0 + per < nrows ? r0 + per : nrows;
-    long long mine = 0;
-    for (int r = r0; r < r1; ++r) mine += group_visible<KVM>(p, p.row_begin + r);
-    long long incl = mine;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const long long o = __shfl_up(incl, d, kWave);
-        if (lane >= d) incl += o;
-    }
-    if (lane == 63) s_scan[wv] = incl;
-    __syncthreads();
-    long long before = 0;
-    for (int i = 0; i < wv; ++i) before += s_scan[i];
-    long long run = before + incl - mine;
-    for (int r = r0; r < r1; ++r) {
-        s_pref[r] = run;
-        run += group_visible<KVM>(p, p.row_begin + r);
-    }
-    long long total = 0;
-    for (int i = 0; i < kWaves; ++i) total += s_scan[i];
-    if (tid == 0) s_pref[nrows] = total;
-    __syncthreads();
-
-    // 2. equal chunks of the (row group, KV head) segments laid end to end
-    const long long Wk = total * NHG;
-    const long long ng = (Wk + p.min_keys - 1) / p.min_keys;
-    const int geff = Wk == 0 ? 0 : (int)(ng < p.nwg ? ng : p.nwg);
-    const long long chunk = geff ? (Wk + geff - 1) / geff : 1;
-    if (blockIdx.x == 0) {
-        for (int sg = tid; sg < nrows * NHG; sg += blockDim.x) {
-            const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
-            const long long V = s_pref[r + 1] - s_pref[r];
-            int base = 0, cnt = 0;
-            if (V > 0) {
-                const long long stt = NHG * s_pref[r] + hg * V;
-                const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
-                cnt = (int)(gl - gf + 1);
-                base = (int)gf + sg;
-            }
-            p.dir[2 * sg] = base;
-            p.dir[2 * sg + 1] = cnt;
-        }
-    }
-    const int gidx = blockIdx.x;
-    if (gidx >= geff) return;
-    long long u = gidx * chunk;
-    const long long uend = u + chunk < Wk ? u + chunk : Wk;
-    int lo = 0, hi = nrows - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (NHG * s_pref[mid] <= u) lo = mid;
-        else hi = mid - 1;
-    }
-    int r = lo;
-    while (u < uend && r < nrows) {
-        const long long rs = NHG * s_pref[r];
-        const long long V = s_pref[r + 1] - s_pref[r];
-        if (V == 0 || u >= rs + NHG * V) {
-            ++r;
-            continue;
-        }
-        const long long rel = u - rs;
-        const int hg = (int)(rel / V);
-        const long long v0 = rel - hg * V;
-        const long long segend = (long long)(hg + 1) * V;
-        const long long lim = (uend - rs < segend ? uend - rs : segend) - (long long)hg * V;
-        const int sg = r * NHG + hg;
-        const long long stt = rs + hg * V;
-        const long long gf = stt / chunk, gl = (stt + V - 1) / chunk;
-        chunk_piece<DT, QM, KVM>(p, smem, pages, p.row_begin + r, hg, v0, lim, gl == gf, sg + gidx);
-        u = stt + lim;
-    }
+    run_schedule(p, NHG, s_pref, s_scan, [&](int rg) { return group_visible<KVM>(p, rg); },
+                 [&](int rg, int hg, long long v0, long long v1, bool fin, int slot) {
+                     chunk_piece<DT, QM, KVM>(p, smem, pages, rg, hg, v0, v1, fin, slot);
+                 });
 }
 
 // Block (segment, token of the block): thread t -> head t/16, dims [(t%16)*8, +8).
@@ -655,6 +586,7 @@ hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& ba
     if (ws_bytes < part_bytes + (size_t)nseg_cap * 2 * 4) return hipErrorInvalidValue;
     p.part = reinterpret_cast<float*>(workspace);
     p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
+    p.piece_cost = chunk::kPieceCost;
     for (long long g0 = 0; g0 < groups_total; g0 += kMaxRows) {
         p.row_begin = (int)g0;
         p.nrows = (int)(groups_total - g0 < kMaxRows ? groups_total - g0 : kMaxRows);

@@ -25,6 +25,7 @@
 //    do (paged_kernel_v21.cuh:307-374).
 #include "dv_common.h"
 #include "dv_device.h"
+#include "dv_schedule.h"
 
 namespace dv {
 
@@ -469,119 +470,8 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
     }
 }
 
-// ---- work schedule ----------------------------------------------------------------
+// ---- work schedule: run_schedule (dv_schedule.h) ------------------------------------
 
-// Every workgroup computes the same schedule from locations / fragment_lengths.
-// The (row, KV-head-group) segments of visible keys are laid end to end, each
-// non-empty one preceded by p.piece_cost keys of "start cost" (the pipeline
-// start of a piece: page ids, query rotation, first loads), and this cost space
-// is cut into equal contiguous chunks, one per workgroup; a workgroup whose
-// chunk crosses into a new segment thus gets fewer real keys.  Per-row cost
-// prefix sums live in LDS (s_pref, nrows + 1 entries).  Workgroup 0 also writes
-// the merge directory (segment -> first partial slot, piece count).  Then
-// piece(row, head_group, v0, v1, final, slot) runs for each piece of this
-// workgroup's chunk; `final` means the segment has no other piece.
-template <int KVM, int RM, class PieceFn>
-__device__ inline void run_schedule(const DecodeParams& p, long long* s_pref, long long* s_scan, PieceFn&& piece) {
-    const int tid = threadIdx.x;
-    const int wv = tid >> 6;
-    const int nthreads = blockDim.x;
-    const int NHG = p.Hkv / p.hpw;
-    const long long c = p.piece_cost;
-
-    // 1. per-row cost (visible keys + start cost, 0 for an empty row) -> exclusive
-    //    prefix sums in LDS
-    const int nrows = p.nrows;
-    const int per = (nrows + nthreads - 1) / nthreads;
-    const int r0 = tid * per;
-    const int r1 = r0 + per < nrows ? r0 + per : nrows;
-    long long mine = 0;
-    for (int r = r0; r < r1; ++r) {
-        const long long v = row_visible<KVM, RM>(p, p.row_begin + r);
-        const long long d = v > 0 ? v + c : 0;
-        s_pref[r] = d;  // the row's cost, replaced by its prefix below
-        mine += d;
-    }
-    const int lane = tid & 63;
-    long long incl = mine;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const long long o = __shfl_up(incl, d, kWave);
-        if (lane >= d) incl += o;
-    }
-    if (lane == 63) s_scan[wv] = incl;
-    __syncthreads();
-    long long before = 0;
-    for (int i = 0; i < wv; ++i) before += s_scan[i];
-    long long run = before + incl - mine;
-    for (int r = r0; r < r1; ++r) {
-        const long long d = s_pref[r];
-        s_pref[r] = run;
-        run += d;
-    }
-    long long total = 0;
-    for (int i = 0; i < nthreads / kWave; ++i) total += s_scan[i];
-    if (tid == 0) s_pref[nrows] = total;
-    __syncthreads();
-
-    // 2. equal chunks of the cost space; segment (r, hg) spans D_r cost units at
-    //    NHG*pref[r] + hg*D_r, its keys the last D_r - c of them
-    const long long Wc = total * NHG;
-    const int geff = Wc == 0 ? 0
-                             : (int)((Wc + p.min_keys - 1) / p.min_keys < p.nwg ? (Wc + p.min_keys - 1) / p.min_keys
-                                                                                : p.nwg);
-    const long long chunk = geff ? (Wc + geff - 1) / geff : 1;
-
-    if (blockIdx.x == 0) {
-        for (int sg = tid; sg < nrows * NHG; sg += nthreads) {
-            const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
-            const long long D = s_pref[r + 1] - s_pref[r];
-            int base = 0, cnt = 0;
-            if (D > 0) {
-                const long long segc = NHG * s_pref[r] + hg * D;
-                const long long gf = (segc + c) / chunk, gl = (segc + D - 1) / chunk;
-                cnt = (int)(gl - gf + 1);
-                base = (int)gf + sg;
-            }
-            p.dir[2 * sg] = base;
-            p.dir[2 * sg + 1] = cnt;
-        }
-    }
-    const int gidx = blockIdx.x;
-    if (gidx >= geff) return;
-
-    long long u = gidx * chunk;
-    const long long uend = u + chunk < Wc ? u + chunk : Wc;
-    // last row r with NHG*pref[r] <= u
-    int lo = 0, hi = nrows - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (NHG * s_pref[mid] <= u) lo = mid;
-        else hi = mid - 1;
-    }
-    int r = lo;
-    while (u < uend && r < nrows) {
-        const long long rs = NHG * s_pref[r];
-        const long long D = s_pref[r + 1] - s_pref[r];
-        if (D == 0 || u >= rs + NHG * D) {
-            ++r;
-            continue;
-        }
-        const int hg = (int)((u - rs) / D);
-        const long long segc = rs + hg * D;  // the segment's cost range [segc, segc + D)
-        const long long ka = segc + c;       // its keys: cost positions [ka, segc + D)
-        const long long a = u > ka ? u : ka;
-        const long long b = uend < segc + D ? uend : segc + D;
-        if (a < b) {
-            const int sg = r * NHG + hg;
-            const long long gf = ka / chunk, gl = (segc + D - 1) / chunk;
-            const int cnt = (int)(gl - gf + 1);
-            const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
-            piece(p.row_begin + r, hg, a - ka, b - ka, cnt == 1, slot);
-        }
-        u = segc + D;
-    }
-}
 
 // ---- the fp32 decode kernel --------------------------------------------------------
 
@@ -593,7 +483,8 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
     const int HPW = p.hpw;
     long long* s_pref = reinterpret_cast<long long*>(smem + HPW * vt_bytes<DT>());
     unsigned char* vt = smem + wv * vt_bytes<DT>();
-    run_schedule<KVM, RM>(p, s_pref, s_scan, [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
+    run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<KVM, RM>(p, row); },
+                 [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
         if (wv < HPW) process_piece<DT, QM, KVM, RM>(p, vt, row, hg * HPW + wv, v0, v1, fin, slot, wv);
     });
 }
@@ -855,7 +746,8 @@ __global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
     const int HPW = p.hpw;
     long long* s_pref = reinterpret_cast<long long*>(smem + HPW * stream::kWaveLds);
     unsigned char* wlds = smem + wv * stream::kWaveLds;
-    run_schedule<KVM, RM>(p, s_pref, s_scan, [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
+    run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<KVM, RM>(p, row); },
+                 [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
         if (wv < HPW) stream::piece<DT, QM, KVM, RM>(p, wlds, row, hg * HPW + wv, v0, v1, fin, slot, wv);
     });
 }

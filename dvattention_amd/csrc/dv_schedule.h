@@ -1,0 +1,123 @@
+// Work split shared by the decode and chunk kernels.
+#pragma once
+
+#include "dv_common.h"
+#include "dv_device.h"
+
+namespace dv {
+
+// Every workgroup computes the same schedule from the per-row visible key
+// counts (row_keys(absolute row), rows [p.row_begin, p.row_begin + p.nrows)).
+// The (row, head-group) segments are laid end to end, each non-empty one
+// preceded by p.piece_cost keys of "start cost" (the pipeline start of a piece:
+// page ids, query rotation, first loads), and this cost space is cut into equal
+// contiguous chunks, one per workgroup; a workgroup whose chunk crosses into a
+// new segment thus gets fewer real keys.  Per-row cost prefix sums live in LDS
+// (s_pref, nrows + 1 entries; s_scan: one entry per wave).  Workgroup 0 writes
+// the merge directory (segment -> first partial slot, piece count).  Then
+// piece(row, head_group, v0, v1, final, slot) runs for each piece of this
+// workgroup's chunk: visible keys [v0, v1) of the segment, `final` when the
+// segment has no other piece, `slot` its partial slot.  Slots are
+// sg + workgroup index, increasing along the cost space, so they are unique and
+// below nwg + nrows * NHG.
+template <class RowKeys, class PieceFn>
+__device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s_pref, long long* s_scan,
+                                    RowKeys&& row_keys, PieceFn&& piece) {
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6;
+    const int nthreads = blockDim.x;
+    const long long c = p.piece_cost;
+
+    // 1. per-row cost (visible keys + start cost, 0 for an empty row) -> exclusive
+    //    prefix sums in LDS
+    const int nrows = p.nrows;
+    const int per = (nrows + nthreads - 1) / nthreads;
+    const int r0 = tid * per;
+    const int r1 = r0 + per < nrows ? r0 + per : nrows;
+    long long mine = 0;
+    for (int r = r0; r < r1; ++r) {
+        const long long v = row_keys(p.row_begin + r);
+        const long long d = v > 0 ? v + c : 0;
+        s_pref[r] = d;  // the row's cost, replaced by its prefix below
+        mine += d;
+    }
+    const int lane = tid & 63;
+    long long incl = mine;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const long long o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += o;
+    }
+    if (lane == 63) s_scan[wv] = incl;
+    __syncthreads();
+    long long before = 0;
+    for (int i = 0; i < wv; ++i) before += s_scan[i];
+    long long run = before + incl - mine;
+    for (int r = r0; r < r1; ++r) {
+        const long long d = s_pref[r];
+        s_pref[r] = run;
+        run += d;
+    }
+    long long total = 0;
+    for (int i = 0; i < nthreads / kWave; ++i) total += s_scan[i];
+    if (tid == 0) s_pref[nrows] = total;
+    __syncthreads();
+
+    // 2. equal chunks of the cost space; segment (r, hg) spans D_r cost units at
+    //    NHG*pref[r] + hg*D_r, its keys the last D_r - c of them
+    const long long Wc = total * NHG;
+    const long long ng = (Wc + p.min_keys - 1) / p.min_keys;
+    const int geff = Wc == 0 ? 0 : (int)(ng < p.nwg ? ng : p.nwg);
+    const long long chunk = geff ? (Wc + geff - 1) / geff : 1;
+
+    if (blockIdx.x == 0) {
+        for (int sg = tid; sg < nrows * NHG; sg += nthreads) {
+            const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
+            const long long D = s_pref[r + 1] - s_pref[r];
+            int base = 0, cnt = 0;
+            if (D > 0) {
+                const long long segc = NHG * s_pref[r] + hg * D;
+                const long long gf = (segc + c) / chunk, gl = (segc + D - 1) / chunk;
+                cnt = (int)(gl - gf + 1);
+                base = (int)gf + sg;
+            }
+            p.dir[2 * sg] = base;
+            p.dir[2 * sg + 1] = cnt;
+        }
+    }
+    const int gidx = blockIdx.x;
+    if (gidx >= geff) return;
+
+    long long u = gidx * chunk;
+    const long long uend = u + chunk < Wc ? u + chunk : Wc;
+    // last row r with NHG*pref[r] <= u
+    int lo = 0, hi = nrows - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (NHG * s_pref[mid] <= u) lo = mid;
+        else hi = mid - 1;
+    }
+    int r = lo;
+    while (u < uend && r < nrows) {
+        const long long rs = NHG * s_pref[r];
+        const long long D = s_pref[r + 1] - s_pref[r];
+        if (D == 0 || u >= rs + NHG * D) {
+            ++r;
+            continue;
+        }
+        const int hg = (int)((u - rs) / D);
+        const long long segc = rs + hg * D;  // the segment's cost range [segc, segc + D)
+        const long long ka = segc + c;       // its keys: cost positions [ka, segc + D)
+        const long long a = u > ka ? u : ka;
+        const long long b = uend < segc + D ? uend : segc + D;
+        if (a < b) {
+            const int sg = r * NHG + hg;
+            const long long gf = ka / chunk, gl = (segc + D - 1) / chunk;
+            const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
+            piece(p.row_begin + r, hg, a - ka, b - ka, gl == gf, slot);
+        }
+        u = segc + D;
+    }
+}
+
+}  // namespace dv
