@@ -10,7 +10,9 @@ steps are timed back to back between two synchronisations; ``value`` is the
 achieved algorithmic HBM rate in TB/s and ``ms_per_step`` the time per call.
 Inputs rotate over enough replicas that consecutive calls never find their K/V
 in the 256 MB Infinity Cache (cold HBM reads, as in a real multi-layer decode
-step).  Every configuration is also reported under ``per_config``.
+step).  Every configuration is also reported under ``per_config``, and the
+cache-side kernels around the path (K-side append, merge_caches re-rotation,
+view metadata) under ``cache_rows``.
 
 ``roofline`` covers the decode kernel family (decode + split-merge launch of one
 call), timed with HIP events on the stream the kernels run on; ``traffic`` is the
@@ -105,6 +107,96 @@ def time_config(i: int, steps: int, warmup: int, device) -> dict:
     return res
 
 
+def _time_calls(fn, n_inputs: int, steps: int, warmup: int) -> tuple:
+    """Mean µs per call of fn(j % n_inputs): (a) `steps` eager back-to-back calls
+    (HIP events; small kernels are bound by the host's launch rate there) and
+    (b) the same calls captured in one HIP graph and replayed (the GPU-side cost
+    of a call, as in a graph-captured decode step)."""
+    for j in range(warmup):
+        fn(j % n_inputs)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for j in range(steps):
+        fn(j % n_inputs)
+    b.record(stream)
+    torch.cuda.synchronize()
+    eager = a.elapsed_time(b) * 1e3 / steps
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for j in range(steps):
+            fn(j % n_inputs)
+    graph.replay()
+    torch.cuda.synchronize()
+    a.record(stream)
+    graph.replay()
+    b.record(stream)
+    torch.cuda.synchronize()
+    replay = a.elapsed_time(b) * 1e3 / steps
+    del graph
+    return replay, eager
+
+
+def time_cache_rows(device, steps: int, warmup: int) -> list:
+    """The rows around the decode path: the K-side append (key rotation + page
+    writes) at a decode step of configuration 2 and at an 8192-token prefill,
+    merge_caches' re-rotation of a 32768-token source, and the on-device view
+    metadata of a configuration-2 step with 4 views.  Algorithmic bytes: keys and
+    values read once and written once, cos/sin, positions and table entries read
+    once (metadata: lengths/orders read, locations and cos/sin written)."""
+    import dvattention_amd as dv
+    g = torch.Generator(device="cpu").manual_seed(7)
+    rows = []
+
+    def append_case(name, W, S, Hkv, cos_rows, n_in, merge=False):
+        E, bs = 128, 16
+        maxB = -(-S // bs)
+        P = W * maxB
+        bt = torch.randperm(P, generator=g).to(torch.int32).reshape(W, maxB).to(device)
+        kc = torch.empty(P, bs, Hkv, E, dtype=torch.bfloat16, device=device)
+        vc = torch.empty_like(kc)
+        pos = torch.arange(S, dtype=torch.int32).repeat(W, 1).to(device)
+        ins = []
+        for _ in range(n_in):
+            k = torch.randn(W, S, Hkv, E, device=device).to(torch.bfloat16).transpose(1, 2)  # k_proj view
+            v = torch.randn(W, S, Hkv, E, device=device).to(torch.bfloat16).transpose(1, 2)
+            c = torch.rand(1 if merge else W, cos_rows, 128, device=device)
+            ins.append((k, v, c, c.clone()))
+
+        def fn(j):
+            k, v, c, sn = ins[j]
+            dv.dvattn_paged_kv_append(k, v, pos, c, sn, kc, vc, bt)
+
+        us, eager = _time_calls(fn, n_in, steps, warmup)
+        kv = W * S * Hkv * E * 2
+        alg = 4 * kv + 2 * ins[0][2].numel() * 4 + W * S * 4 + W * maxB * 4
+        rows.append({"row": name, "us_per_call": round(us, 2), "us_per_call_eager": round(eager, 2), "alg_bytes": alg,
+                     "achieved_GBs": round(alg / (us * 1e-6) / 1e9, 1),
+                     "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+        del ins, kc, vc
+
+    append_case("kv_append_decode_cfg2 (W=32,S=1,Hkv=8)", 32, 1, 8, 1, 4)
+    append_case("kv_append_prefill (W=1,S=8192,Hkv=8)", 1, 8192, 8, 8192, 4)
+    append_case("merge_caches (L=32768,Hkv=8, one cos/sin row)", 1, 32768, 8, 1, 2, merge=True)
+    F, W, S, R = 4, 32, 1, 128
+    fl = torch.tensor([4096, 512, 2048, 1], dtype=torch.int32, device=device)
+    order = torch.stack([torch.randperm(F, generator=g) for _ in range(W)]).to(torch.int32).to(device)
+    inv = (1.0 / (1e4 ** (torch.arange(0, R, 2, dtype=torch.float) / R))).to(device)
+    loc = torch.empty(F, W, S, dtype=torch.int32, device=device)
+    cos = torch.empty(F, W, S, R, device=device)
+    sin = torch.empty_like(cos)
+    us, eager = _time_calls(
+        lambda j: torch.ops.libdvatt.dvattn_view_metadata(loc, cos, sin, fl, order, inv, 1.0, None), 1, steps, warmup)
+    alg = F * 4 + W * F * 4 + R // 2 * 4 + loc.numel() * 4 + 2 * cos.numel() * 4
+    rows.append({"row": f"view_metadata (F={F},W={W},S={S},R={R})", "us_per_call": round(us, 2),
+                 "us_per_call_eager": round(eager, 2), "alg_bytes": alg,
+                 "achieved_GBs": round(alg / (us * 1e-6) / 1e9, 1),
+                 "hbm_frac": round(alg / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+    torch.cuda.empty_cache()
+    return rows
+
+
 def measure_copy(device, nbytes: int = 1 << 30, reps: int = 10) -> float:
     """Achievable HBM rate of a plain device-to-device copy (read + write bytes / time)."""
     src = torch.empty(nbytes, dtype=torch.uint8, device=device)
@@ -174,6 +266,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="1,2,3,4,5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-cache-rows", action="store_true", help="skip the K-side append / view metadata rows")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the operator has no multi-GPU path); "
@@ -194,6 +287,10 @@ def main() -> int:
         log(f"[bench] cfg{i} {r['workload']}: {r['us_per_call']} us/call (events, back-to-back), "
             f"kernel {r['kernel_us_mean']} us, {r['achieved_GBs']} GB/s = {100 * r['hbm_frac']:.1f}% HBM, "
             f"{r['achieved_TFLOPs']} TFLOP/s")
+    cache_rows = [] if args.no_cache_rows else time_cache_rows(device, args.steps, args.warmup)
+    for r in cache_rows:
+        log(f"[bench] {r['row']}: {r['us_per_call']} us/call in a graph ({r['us_per_call_eager']} eager), "
+            f"{r['achieved_GBs']} GB/s = {100 * r['hbm_frac']:.1f}% HBM")
     head = per[2]
     # HBM bytes per call from the committed rocprofv3 --pmc summary (FETCH_SIZE / WRITE_SIZE
     # scaled by a 1 GiB copy); absent -> null
@@ -228,6 +325,7 @@ def main() -> int:
                      "launch_us": head["kernel_us_mean"], "copy_GBs": round(copy_gbs, 1)},
         "cpu_baseline": cpu,
         "per_config": [per[i] for i in sorted(per)],
+        "cache_rows": cache_rows,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -35,24 +35,30 @@ _load_ops()
 from .attention import (  # noqa: E402
     apply_rotary_pos_emb,
     dvattn_fused,
+    dvattn_paged_kv_append,
     dvattn_paged_sdpa,
     dvattn_rope,
     dvattn_sdpa,
     dvattn_sdpa_pt,
     dvattn_varlen_paged_sdpa,
     dvattn_varlen_rope,
+    dvattn_view_metadata,
+    merge_caches_paged,
     rotate_half,
 )
 
 __all__ = [
     "apply_rotary_pos_emb",
     "dvattn_fused",
+    "dvattn_paged_kv_append",
     "dvattn_paged_sdpa",
     "dvattn_rope",
     "dvattn_sdpa",
     "dvattn_sdpa_pt",
     "dvattn_varlen_paged_sdpa",
     "dvattn_varlen_rope",
+    "dvattn_view_metadata",
+    "merge_caches_paged",
     "rotate_half",
     "TORCH_OPS_LIBRARY",
     "CAPI_LIBRARY",

@@ -26,7 +26,7 @@ ARCH = os.environ.get("DVATTN_ARCH", "gfx950")
 CAPI_SO = os.path.join(HERE, "libdvattn_amd.so")
 TORCH_SO = os.path.join(HERE, "_libdvatt.so")
 
-HIP_SOURCES = ["dv_decode.hip", "dv_chunk.hip", "dv_rope.hip", "dv_capi.hip"]
+HIP_SOURCES = ["dv_decode.hip", "dv_chunk.hip", "dv_rope.hip", "dv_cache.hip", "dv_capi.hip"]
 
 # gfx950 code only; packed-fp32 instructions are disabled (the host pass of
 # hipcc warns that it does not know the feature, which is harmless).

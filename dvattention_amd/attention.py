@@ -89,6 +89,69 @@ def dvattn_varlen_paged_sdpa(queries: torch.Tensor, locations: torch.Tensor, cos
     return out
 
 
+def dvattn_paged_kv_append(keys: torch.Tensor, values: torch.Tensor, positions: torch.Tensor,
+                           cosines: torch.Tensor, sines: torch.Tensor, k_cache: torch.Tensor,
+                           v_cache: torch.Tensor, block_tables: torch.Tensor):
+    """The K side of a decode step on a paged cache: rotate the new keys with the
+    model's (cos, sin) and write keys and values into their pages (the reference
+    rotates ``key_states`` at attention.py:304 and appends them to the sequence's
+    own cache at attention.py:141-152).
+
+    keys/values ``[W,Hkv,S,E]`` (strided views such as k_proj's output
+    transposed are fine), positions ``[W,S]`` int32 logical positions in each
+    sequence's token stream (negative: masked, not written), cosines/sines
+    ``[W,S,R]`` / ``[S,R]`` / ``[R]`` in float32 or the model dtype, read in full
+    (``apply_rotary_pos_emb``, attention.py:82-88, evaluated with PyTorch's
+    rounding).  Caches ``[num_blocks, block_size, Hkv, E]`` are updated in place.
+    """
+    W, _, S, _ = keys.shape
+    R = cosines.size(-1)
+    cos = cosines.reshape((1,) * (3 - cosines.dim()) + tuple(cosines.shape)) if cosines.dim() < 3 else cosines
+    sin = sines.reshape((1,) * (3 - sines.dim()) + tuple(sines.shape)) if sines.dim() < 3 else sines
+    cos = cos.expand(W, S, R)
+    sin = sin.expand(W, S, R)
+    torch.ops.libdvatt.dvattn_paged_kv_append(k_cache, v_cache, block_tables, positions, keys, values, cos, sin)
+    return k_cache, v_cache
+
+
+def merge_caches_paged(source_keys: torch.Tensor, source_values: torch.Tensor, offset_cos: torch.Tensor,
+                       offset_sin: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       block_tables: torch.Tensor, positions: torch.Tensor):
+    """``merge_caches`` (attention.py:245-251) into a paged target: the source
+    keys ``[1,Hkv,L,E]`` are re-rotated by the target's length (one cos/sin row,
+    ``offset_cos``/``offset_sin`` ``[R]``: the rotary embedding at that length)
+    and written with the source values at ``positions`` ``[1,L]`` (the target's
+    next L logical positions)."""
+    return dvattn_paged_kv_append(source_keys, source_values, positions, offset_cos.reshape(-1),
+                                  offset_sin.reshape(-1), k_cache, v_cache, block_tables)
+
+
+def dvattn_view_metadata(fragment_lengths: torch.Tensor, order: torch.Tensor, num_new_tokens: int,
+                         inv_freq: torch.Tensor, attention_scaling: float = 1.0,
+                         round_to: Optional[torch.dtype] = None):
+    """Per-view locations and query cos/sin for a decode step, on the device
+    (attention.py:158-186).
+
+    fragment_lengths ``[F]`` int32: segment lengths including the new tokens;
+    order ``[W,F]`` int32: sequence w's segments in its own order (view indices,
+    its own segment last); inv_freq ``[R/2]`` float32: the model's rotary inverse
+    frequencies (``model.rotary_emb.inv_freq``).  Returns ``(locations [F,W,S]
+    int32, cosines [F,W,S,R], sines [F,W,S,R])`` float32, ready for
+    ``dvattn_paged_sdpa`` / ``dvattn_fused``.  ``round_to`` rounds cos/sin through
+    the model dtype, as the reference's rotary call does.
+    """
+    F = fragment_lengths.numel()
+    W = order.size(0)
+    R = 2 * inv_freq.numel()
+    dev = fragment_lengths.device
+    loc = torch.empty((F, W, num_new_tokens), dtype=torch.int32, device=dev)
+    cos = torch.empty((F, W, num_new_tokens, R), dtype=torch.float32, device=dev)
+    sin = torch.empty_like(cos)
+    torch.ops.libdvatt.dvattn_view_metadata(loc, cos, sin, fragment_lengths, order, inv_freq,
+                                            float(attention_scaling), round_to)
+    return loc, cos, sin
+
+
 def dvattn_sdpa_pt(queries: torch.Tensor, locations: torch.Tensor, keys: list, values: list,
                    scale: float, return_intermediate_results: bool = False):
     """The reference's pure-PyTorch debugging helper (attention.py:36-65), kept
@@ -134,4 +197,5 @@ def apply_rotary_pos_emb(x, cos, sin, unsqueeze_dim=1):
 __all__ = [
     "dvattn_fused", "dvattn_sdpa", "dvattn_rope", "dvattn_varlen_rope", "dvattn_paged_sdpa",
     "dvattn_varlen_paged_sdpa", "dvattn_sdpa_pt", "rotate_half", "apply_rotary_pos_emb",
+    "dvattn_paged_kv_append", "merge_caches_paged", "dvattn_view_metadata",
 ]

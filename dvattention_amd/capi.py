@@ -28,6 +28,7 @@ EXPORTED = [
     "dvattn_varlen_paged_sdpa_workspace_size", "dvattn_varlen_paged_sdpa",
     "dvattn_sdpa_workspace_size", "dvattn_sdpa", "dvattn_fused",
     "dvattn_rope", "dvattn_varlen_rope",
+    "dvattn_paged_kv_append", "dvattn_view_metadata",
 ]
 
 
@@ -36,6 +37,14 @@ class Shape(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int) for n in (
         "F", "W", "Hq", "Hkv", "E", "Ev", "S", "block_size", "max_blocks_per_seq",
         "total_q_tokens", "num_blocks", "rotary_dim")]
+
+
+class KvLayout(ctypes.Structure):
+    """dvattn_kv_layout: element strides of keys/values (w, h, s), cos/sin (w, s)
+    and the caches (page, row, head)."""
+    _fields_ = [("key_strides", ctypes.c_longlong * 3), ("value_strides", ctypes.c_longlong * 3),
+                ("rope_strides", ctypes.c_longlong * 2), ("k_cache_strides", ctypes.c_longlong * 3),
+                ("v_cache_strides", ctypes.c_longlong * 3)]
 
 
 class DvattnError(RuntimeError):
@@ -81,6 +90,11 @@ def lib() -> ctypes.CDLL:
         L.dvattn_rope.argtypes = [_I, _VP, _VP, _VP, _VP, _SP, _VP]
         L.dvattn_varlen_rope.restype = _I
         L.dvattn_varlen_rope.argtypes = [_I, _VP, _VP, _VP, _VP, _SP, _VP]
+        L.dvattn_paged_kv_append.restype = _I
+        L.dvattn_paged_kv_append.argtypes = [_I, _I, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SP,
+                                             ctypes.POINTER(KvLayout), _VP]
+        L.dvattn_view_metadata.restype = _I
+        L.dvattn_view_metadata.argtypes = [_VP, _VP, _VP, _VP, _VP, _VP, _F, _I, _I, _I, _I, _I, _VP]
         _lib = L
     return _lib
 
@@ -201,3 +215,37 @@ def varlen_rope(out, queries, cosines, sines):
     _check(lib().dvattn_varlen_rope(dtype_code(out.dtype), _ptr(out), _ptr(queries), _ptr(cosines), _ptr(sines),
                                     ctypes.byref(s), _stream(out)))
     return out
+
+
+def kv_append(k_cache, v_cache, block_tables, positions, keys, values, cosines, sines):
+    """dvattn_paged_kv_append: keys/values [W,Hkv,S,E] (any strides, last dim
+    contiguous), cos/sin [W|1, S|1, R], caches [P,bs,Hkv,E] (strided views allowed)."""
+    W, Hkv, S, E = keys.shape
+    s = Shape(F=0, W=W, Hq=0, Hkv=Hkv, E=E, Ev=values.shape[3], S=S, block_size=k_cache.shape[1],
+              max_blocks_per_seq=block_tables.shape[1], total_q_tokens=0, num_blocks=k_cache.shape[0],
+              rotary_dim=cosines.shape[2])
+    lay = KvLayout()
+    for i in range(3):
+        lay.key_strides[i] = keys.stride(i)
+        lay.value_strides[i] = values.stride(i)
+        lay.k_cache_strides[i] = k_cache.stride(i)
+        lay.v_cache_strides[i] = v_cache.stride(i)
+    lay.rope_strides[0] = 0 if cosines.shape[0] == 1 else cosines.stride(0)
+    lay.rope_strides[1] = 0 if cosines.shape[1] == 1 else cosines.stride(1)
+    dt = dtype_code(k_cache.dtype)
+    rdt = DVATTN_F32 if cosines.dtype == torch.float32 else dtype_code(cosines.dtype)
+    _check(lib().dvattn_paged_kv_append(dt, rdt, _ptr(k_cache), _ptr(v_cache), _ptr(block_tables), _ptr(positions),
+                                        _ptr(keys), _ptr(values), _ptr(cosines), _ptr(sines), ctypes.byref(s),
+                                        ctypes.byref(lay), _stream(k_cache)))
+    return k_cache, v_cache
+
+
+def view_metadata(locations, cosines, sines, fragment_lengths, order, inv_freq, attention_scaling=1.0,
+                  round_to=None):
+    """dvattn_view_metadata: locations [F,W,S] i32, cos/sin [F,W,S,R] f32."""
+    F, W, S = locations.shape
+    rd = -1 if round_to in (None, torch.float32) else dtype_code(round_to)
+    _check(lib().dvattn_view_metadata(_ptr(locations), _ptr(cosines), _ptr(sines), _ptr(fragment_lengths),
+                                      _ptr(order), _ptr(inv_freq), attention_scaling, rd, F, W, S,
+                                      cosines.shape[3], _stream(locations)))
+    return locations, cosines, sines

@@ -377,4 +377,87 @@ dvattn_status dvattn_varlen_rope(int dtype, void* out, const void* queries, cons
     return ok();
 }
 
+// ---------------------------------------------------------------------------
+dvattn_status dvattn_paged_kv_append(int dtype, int rope_dtype, void* k_cache, void* v_cache,
+                                     const int* block_tables, const int* positions, const void* keys,
+                                     const void* values, const void* cosines, const void* sines,
+                                     const dvattn_shape* s, const dvattn_kv_layout* lay, void* stream) {
+    if (!s || !lay) return fail(DVATTN_ERR_INVALID, "shape or layout is null");
+    if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+    if (rope_dtype != DVATTN_F32 && rope_dtype != dtype)
+        return fail(DVATTN_ERR_UNSUPPORTED, "cos/sin dtype code %d must be float32 or the storage dtype %d",
+                    rope_dtype, dtype);
+    if (s->W < 0 || s->S < 0 || s->Hkv < 0 || s->E < 0 || s->Ev < 0)
+        return fail(DVATTN_ERR_INVALID, "negative W/S/Hkv/E/Ev");
+    if ((long long)s->W * s->S * s->Hkv == 0 || (s->E == 0 && s->Ev == 0)) return ok();
+    dvattn_status st;
+    if ((st = check_rotary(s->rotary_dim, s->E)) != DVATTN_OK) return st;
+    if (s->block_size <= 0) return fail(DVATTN_ERR_INVALID, "block_size must be positive (got %d)", s->block_size);
+    if (s->max_blocks_per_seq < 0 || s->num_blocks < 0)
+        return fail(DVATTN_ERR_INVALID, "max_blocks_per_seq / num_blocks must be >= 0");
+    if (!k_cache || !v_cache || !keys || !values || !positions || (s->max_blocks_per_seq > 0 && !block_tables) ||
+        (s->rotary_dim > 0 && (!cosines || !sines)))
+        return fail(DVATTN_ERR_INVALID, "null pointer");
+    dv::AppendParams p;
+    memset(&p, 0, sizeof(p));
+    p.kc = k_cache;
+    p.vc = v_cache;
+    p.bt = block_tables;
+    p.pos = positions;
+    p.k = keys;
+    p.v = values;
+    p.cosv = cosines;
+    p.sinv = sines;
+    for (int i = 0; i < 3; ++i) {
+        p.kcs[i] = lay->k_cache_strides[i];
+        p.vcs[i] = lay->v_cache_strides[i];
+        p.ks[i] = lay->key_strides[i];
+        p.vs[i] = lay->value_strides[i];
+    }
+    p.cs[0] = lay->rope_strides[0];
+    p.cs[1] = lay->rope_strides[1];
+    p.W = s->W;
+    p.S = s->S;
+    p.Hkv = s->Hkv;
+    p.E = s->E;
+    p.Ev = s->Ev;
+    p.R = s->rotary_dim;
+    p.bs = s->block_size;
+    p.maxB = s->max_blocks_per_seq;
+    p.nblocks = s->num_blocks;
+    hipError_t e = dv::launch_kv_append(dtype, rope_dtype, p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dvattn_paged_kv_append launch");
+    return ok();
+}
+
+dvattn_status dvattn_view_metadata(int* locations, float* cosines, float* sines, const int* fragment_lengths,
+                                   const int* order, const float* inv_freq, float attention_scaling,
+                                   int round_dtype, int F, int W, int S, int rotary_dim, void* stream) {
+    if (F < 0 || W < 0 || S < 0) return fail(DVATTN_ERR_INVALID, "negative F/W/S");
+    if (rotary_dim < 0 || (rotary_dim & 1))
+        return fail(DVATTN_ERR_UNSUPPORTED, "rotary_dim must be even and >= 0 (got %d)", rotary_dim);
+    if (round_dtype != -1 && round_dtype != DVATTN_F32 && round_dtype != DVATTN_F16 && round_dtype != DVATTN_BF16)
+        return fail(DVATTN_ERR_UNSUPPORTED, "unsupported round_dtype code %d", round_dtype);
+    if ((long long)F * W * S == 0) return ok();
+    if (!locations || !fragment_lengths || !order || (rotary_dim > 0 && (!cosines || !sines || !inv_freq)))
+        return fail(DVATTN_ERR_INVALID, "null pointer");
+    dv::MetaParams p;
+    memset(&p, 0, sizeof(p));
+    p.loc = locations;
+    p.cosv = cosines;
+    p.sinv = sines;
+    p.fl = fragment_lengths;
+    p.order = order;
+    p.inv_freq = inv_freq;
+    p.scaling = attention_scaling;
+    p.round_dt = round_dtype == DVATTN_F32 ? -1 : round_dtype;
+    p.F = F;
+    p.W = W;
+    p.S = S;
+    p.R = rotary_dim;
+    hipError_t e = dv::launch_view_meta(p, (hipStream_t)stream);
+    if (e != hipSuccess) return hip_fail(e, "dvattn_view_metadata launch");
+    return ok();
+}
+
 }  // extern "C"

@@ -84,6 +84,36 @@ struct RopeParams {
     int half_width;       // 1: cos/sin rows hold R/2 entries (varlen layout)
 };
 
+// K/V append: new tokens' keys (rotated) and values written into their cache rows.
+struct AppendParams {
+    void* kc;                 // destination caches, element strides (page, row, head), last dim contiguous
+    void* vc;
+    long long kcs[3], vcs[3];
+    const int* bt;            // block_tables [W, maxB]
+    const int* pos;           // positions [W, S]: logical position of each new token (< 0: not written)
+    const void* k;            // keys [W, Hkv, S, E], element strides (w, h, s)
+    const void* v;            // values [W, Hkv, S, Ev]
+    long long ks[3], vs[3];
+    const void* cosv;         // cos/sin [W, S, R], element strides (w, s); 0 broadcasts
+    const void* sinv;
+    long long cs[2];
+    int W, S, Hkv, E, Ev, R;
+    int bs, maxB, nblocks;
+};
+
+// View metadata: per (view, sequence, new token) location and rotary cos/sin.
+struct MetaParams {
+    int* loc;                 // [F, W, S]
+    float* cosv;              // [F, W, S, R] (full width, both halves equal)
+    float* sinv;
+    const int* fl;            // fragment_lengths [F]
+    const int* order;         // [W, F]: view index of sequence w's j-th segment
+    const float* inv_freq;    // [R/2]
+    float scaling;            // attention scaling applied to cos and sin
+    int round_dt;             // -1, or a 16-bit dtype code the values are rounded through
+    int F, W, S, R;
+};
+
 // Internal launchers (return a hipError_t; argument validation happens in the C ABI).
 size_t decode_workspace_bytes(int nrows_total, int Hkv, int device, int dtype);
 // max_keys_per_row: host-known upper bound of the visible keys of one row (sizes
@@ -92,6 +122,9 @@ hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const De
                          int nrows_total, long long max_keys_per_row, void* workspace, size_t ws_bytes,
                          hipStream_t stream);
 hipError_t launch_rope(int dtype, const RopeParams& p, hipStream_t stream);
+// rope_dtype: kF32, or the storage dtype (cos/sin in the model's dtype).
+hipError_t launch_kv_append(int dtype, int rope_dtype, const AppendParams& p, hipStream_t stream);
+hipError_t launch_view_meta(const MetaParams& p, hipStream_t stream);
 
 // Multi-query path (S >= 2 tokens per sequence, 16-bit types): K/V read once per
 // block of 16 tokens.  Rows of DecodeParams are (sequence, 16-token block) groups.

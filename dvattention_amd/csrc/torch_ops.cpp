@@ -428,6 +428,151 @@ void dvattn_fused_op(at::Tensor& out, at::Tensor& rq, double scale, const at::Te
     sdpa_common(out, scale, locations, rq, fragment_lengths, ks, vs, &queries, &rq, &cosines, &sines);
 }
 
+// ---------------------------------------------------------------------------
+// dvattn_paged_kv_append(Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor block_tables,
+//   Tensor positions, Tensor keys, Tensor values, Tensor cosines, Tensor sines)
+// The K side of a decode step (attention.py:304 rotation + 141-152 cache append)
+// and merge_caches' re-rotation (attention.py:245-251) on a paged cache.
+// keys/values [W,Hkv,S,E|Ev] and the caches may be strided views (last dim
+// contiguous); cos/sin [W|1, S|1, R] broadcast over size-1 dims.
+void dvattn_paged_kv_append_op(at::Tensor& k_cache, at::Tensor& v_cache, const at::Tensor& block_tables,
+                               const at::Tensor& positions, const at::Tensor& keys, const at::Tensor& values,
+                               const at::Tensor& cosines, const at::Tensor& sines) {
+    const int dt = dtype_code(k_cache);
+    check_dim(k_cache, 4, "k_cache");
+    check_dim(v_cache, 4, "v_cache");
+    check_dim(block_tables, 2, "block_tables");
+    check_dim(positions, 2, "positions");
+    check_dim(keys, 4, "keys");
+    check_dim(values, 4, "values");
+    check_dim(cosines, 3, "cosines");
+    check_dim(sines, 3, "sines");
+    check_same(v_cache, k_cache, "v_cache");
+    check_same(keys, k_cache, "keys");
+    check_same(values, k_cache, "values");
+    check_i32(block_tables, "block_tables");
+    check_i32(positions, "positions");
+    TORCH_CHECK(cosines.scalar_type() == at::kFloat || cosines.scalar_type() == k_cache.scalar_type(),
+                "dvattn_paged_kv_append: cosines must be float32 or ", k_cache.scalar_type(), ", got ",
+                cosines.scalar_type());
+    check_same(sines, cosines, "sines");
+    const at::Tensor* all[] = {&k_cache, &v_cache, &block_tables, &positions, &keys, &values, &cosines, &sines};
+    const char* names[] = {"k_cache", "v_cache", "block_tables", "positions", "keys", "values", "cosines", "sines"};
+    for (int i = 0; i < 8; ++i) check_dev(*all[i], k_cache, names[i]);
+    check_contig(block_tables, "block_tables");
+    check_contig(positions, "positions");
+    for (int i : {0, 1, 4, 5})
+        TORCH_CHECK(all[i]->size(3) <= 1 || all[i]->stride(3) == 1, "dvattn_paged_kv_append: the last dim of ",
+                    names[i], " must be contiguous");
+    for (int i : {6, 7})
+        TORCH_CHECK(all[i]->size(2) <= 1 || all[i]->stride(2) == 1, "dvattn_paged_kv_append: the last dim of ",
+                    names[i], " must be contiguous");
+    TORCH_CHECK(!keys.is_alias_of(k_cache) && !values.is_alias_of(v_cache) && !keys.is_alias_of(v_cache) &&
+                    !values.is_alias_of(k_cache),
+                "dvattn_paged_kv_append: keys/values must not share storage with the caches");
+    const int64_t W = keys.size(0), Hkv = keys.size(1), S = keys.size(2), E = keys.size(3);
+    const int64_t Ev = values.size(3);
+    TORCH_CHECK(values.size(0) == W && values.size(1) == Hkv && values.size(2) == S,
+                "dvattn_paged_kv_append: values must be [W,Hkv,S,Ev] = [", W, ",", Hkv, ",", S, ",Ev], got ",
+                values.sizes());
+    const int64_t P = k_cache.size(0), bs = k_cache.size(1);
+    TORCH_CHECK(k_cache.size(2) == Hkv && k_cache.size(3) == E,
+                "dvattn_paged_kv_append: k_cache must be [num_blocks, block_size, Hkv, E] with Hkv=", Hkv, ", E=", E,
+                ", got ", k_cache.sizes());
+    TORCH_CHECK(v_cache.size(0) == P && v_cache.size(1) == bs && v_cache.size(2) == Hkv && v_cache.size(3) == Ev,
+                "dvattn_paged_kv_append: v_cache must be [num_blocks, block_size, Hkv, Ev], got ", v_cache.sizes());
+    TORCH_CHECK(positions.size(0) == W && positions.size(1) == S, "dvattn_paged_kv_append: positions must be [W,S] = [",
+                W, ",", S, "], got ", positions.sizes());
+    TORCH_CHECK(block_tables.size(0) >= W, "dvattn_paged_kv_append: block_tables needs a row per sequence (", W,
+                "), got ", block_tables.sizes());
+    const int64_t R = cosines.size(2);
+    TORCH_CHECK((cosines.size(0) == W || cosines.size(0) == 1) && (cosines.size(1) == S || cosines.size(1) == 1),
+                "dvattn_paged_kv_append: cosines must be [W|1, S|1, R], got ", cosines.sizes());
+    TORCH_CHECK(sines.sizes() == cosines.sizes(), "dvattn_paged_kv_append: sines must match cosines, got ",
+                sines.sizes());
+    TORCH_CHECK(R <= E && R % 2 == 0, "dvattn_paged_kv_append: rotary dim ", R, " must be even and <= E=", E);
+    TORCH_CHECK(cosines.stride(0) == sines.stride(0) && cosines.stride(1) == sines.stride(1),
+                "dvattn_paged_kv_append: cosines and sines must have the same strides");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(k_cache.device());
+    dvattn_shape s{};
+    s.W = as_int(W, "W");
+    s.S = as_int(S, "S");
+    s.Hkv = as_int(Hkv, "Hkv");
+    s.E = as_int(E, "E");
+    s.Ev = as_int(Ev, "Ev");
+    s.block_size = as_int(bs, "block_size");
+    s.max_blocks_per_seq = as_int(block_tables.size(1), "max_blocks_per_seq");
+    s.num_blocks = as_int(P, "num_blocks");
+    s.rotary_dim = as_int(R, "rotary_dim");
+    dvattn_kv_layout lay{};
+    for (int i = 0; i < 3; ++i) {
+        lay.key_strides[i] = keys.stride(i);
+        lay.value_strides[i] = values.stride(i);
+        lay.k_cache_strides[i] = k_cache.stride(i);
+        lay.v_cache_strides[i] = v_cache.stride(i);
+    }
+    lay.rope_strides[0] = cosines.size(0) == 1 ? 0 : cosines.stride(0);
+    lay.rope_strides[1] = cosines.size(1) == 1 ? 0 : cosines.stride(1);
+    const int rope_dt = cosines.scalar_type() == at::kFloat ? DVATTN_F32 : dt;
+    check_status(dvattn_paged_kv_append(dt, rope_dt, k_cache.data_ptr(), v_cache.data_ptr(),
+                                        block_tables.data_ptr<int>(), positions.data_ptr<int>(), keys.data_ptr(),
+                                        values.data_ptr(), cosines.data_ptr(), sines.data_ptr(), &s, &lay,
+                                        stream_of(k_cache)),
+                 "dvattn_paged_kv_append");
+}
+
+// dvattn_view_metadata(Tensor(a!) locations, Tensor(b!) cosines, Tensor(c!) sines,
+//   Tensor fragment_lengths, Tensor order, Tensor inv_freq, float attention_scaling,
+//   ScalarType? round_to=None)        attention.py:158-186
+void dvattn_view_metadata_op(at::Tensor& locations, at::Tensor& cosines, at::Tensor& sines,
+                             const at::Tensor& fragment_lengths, const at::Tensor& order, const at::Tensor& inv_freq,
+                             double attention_scaling, std::optional<at::ScalarType> round_to) {
+    check_dim(locations, 3, "locations");
+    check_dim(cosines, 4, "cosines");
+    check_dim(sines, 4, "sines");
+    check_dim(fragment_lengths, 1, "fragment_lengths");
+    check_dim(order, 2, "order");
+    check_dim(inv_freq, 1, "inv_freq");
+    check_i32(locations, "locations");
+    check_i32(fragment_lengths, "fragment_lengths");
+    check_i32(order, "order");
+    check_f32(cosines, "cosines");
+    check_f32(sines, "sines");
+    check_f32(inv_freq, "inv_freq");
+    const at::Tensor* all[] = {&locations, &cosines, &sines, &fragment_lengths, &order, &inv_freq};
+    const char* names[] = {"locations", "cosines", "sines", "fragment_lengths", "order", "inv_freq"};
+    for (int i = 0; i < 6; ++i) {
+        check_contig(*all[i], names[i]);
+        check_dev(*all[i], locations, names[i]);
+    }
+    const int64_t F = locations.size(0), W = locations.size(1), S = locations.size(2), R = cosines.size(3);
+    TORCH_CHECK(cosines.size(0) == F && cosines.size(1) == W && cosines.size(2) == S,
+                "dvattn_view_metadata: cosines must be [F,W,S,R], got ", cosines.sizes());
+    TORCH_CHECK(sines.sizes() == cosines.sizes(), "dvattn_view_metadata: sines must match cosines");
+    TORCH_CHECK(fragment_lengths.size(0) == F, "dvattn_view_metadata: fragment_lengths must be [F], got ",
+                fragment_lengths.sizes());
+    TORCH_CHECK(order.size(0) == W && order.size(1) == F, "dvattn_view_metadata: order must be [W,F], got ",
+                order.sizes());
+    TORCH_CHECK(R % 2 == 0 && inv_freq.size(0) >= R / 2, "dvattn_view_metadata: need an even rotary dim and R/2 ",
+                "inverse frequencies (R=", R, ", got ", inv_freq.size(0), ")");
+    int rd = -1;
+    if (round_to.has_value()) {
+        switch (*round_to) {
+            case at::kFloat: rd = -1; break;
+            case at::kHalf: rd = DVATTN_F16; break;
+            case at::kBFloat16: rd = DVATTN_BF16; break;
+            default: TORCH_CHECK(false, "dvattn_view_metadata: round_to must be float32, float16 or bfloat16");
+        }
+    }
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(locations.device());
+    check_status(dvattn_view_metadata(locations.data_ptr<int>(), cosines.data_ptr<float>(), sines.data_ptr<float>(),
+                                      fragment_lengths.data_ptr<int>(), order.data_ptr<int>(),
+                                      inv_freq.data_ptr<float>(), (float)attention_scaling, rd, as_int(F, "F"),
+                                      as_int(W, "W"), as_int(S, "S"), as_int(R, "rotary_dim"),
+                                      stream_of(locations)),
+                 "dvattn_view_metadata");
+}
+
 }  // namespace
 
 TORCH_LIBRARY(libdvatt, m) {
@@ -452,6 +597,12 @@ TORCH_LIBRARY(libdvatt, m) {
           "Tensor cosines, Tensor sines, Tensor fragment_lengths, Tensor k_cache, Tensor v_cache, "
           "Tensor block_tables, Tensor cu_seqlens_q, Tensor cu_seqlens_k) -> ()",
           tags, torch::_RegisterOrVerify::REGISTER);
+    // around the path: the reference does these in Python (attention.py:141-192, 245-251, 304)
+    m.def("dvattn_paged_kv_append(Tensor(a!) k_cache, Tensor(b!) v_cache, Tensor block_tables, "
+          "Tensor positions, Tensor keys, Tensor values, Tensor cosines, Tensor sines) -> ()");
+    m.def("dvattn_view_metadata(Tensor(a!) locations, Tensor(b!) cosines, Tensor(c!) sines, "
+          "Tensor fragment_lengths, Tensor order, Tensor inv_freq, float attention_scaling, "
+          "ScalarType? round_to=None) -> ()");
 }
 
 TORCH_LIBRARY_IMPL(libdvatt, CUDA, m) {
@@ -461,4 +612,6 @@ TORCH_LIBRARY_IMPL(libdvatt, CUDA, m) {
     m.impl("dvattn_fused", dvattn_fused_op);
     m.impl("dvattn_varlen_rope", dvattn_varlen_rope_op);
     m.impl("dvattn_varlen_paged_sdpa", dvattn_varlen_paged_sdpa_op);
+    m.impl("dvattn_paged_kv_append", dvattn_paged_kv_append_op);
+    m.impl("dvattn_view_metadata", dvattn_view_metadata_op);
 }

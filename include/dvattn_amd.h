@@ -21,6 +21,11 @@
  *   dvattn_rope              <- op `dvattn_rope`, src/binding.cu:414,41-77 (rope_gpu)
  *   dvattn_varlen_rope       <- op `dvattn_varlen_rope`, src/binding.cu:417,205-247
  *   dvattn_shape             <- struct Shape, src/common.h:5-20
+ * and, around the path (the reference does these in Python):
+ *   dvattn_paged_kv_append   <- python/dvattn/attention.py:304 + 141-152 (key rotation and
+ *                               cache append of a decode step), 245-251 (merge_caches)
+ *   dvattn_view_metadata     <- python/dvattn/attention.py:158-186 (per-view locations,
+ *                               cos/sin)
  *
  * Semantics (identical to the reference operators):
  *   - GQA factor 16 (Hq == 16*Hkv) and head dims E == Ev == 128 only; other
@@ -160,6 +165,60 @@ DVATTN_API dvattn_status dvattn_rope(int dtype, void* out, const void* queries, 
                           const float* sines, const dvattn_shape* shape, void* stream);
 DVATTN_API dvattn_status dvattn_varlen_rope(int dtype, void* out, const void* queries, const float* cosines,
                                  const float* sines, const dvattn_shape* shape, void* stream);
+
+/* ---- K side of a decode step: rotate new keys, append K/V into pages --------
+ * For every new token (w, s) with positions[w,s] = p >= 0, page
+ * block_tables[w, p / block_size], row p % block_size:
+ *   k_cache[page, row, h, :] = rope(keys[w, h, s, :], cosines[w, s, :], sines[w, s, :])
+ *   v_cache[page, row, h, :] = values[w, h, s, :]
+ * rope is the reference's apply_rotary_pos_emb (attention.py:82-88): dims e < R
+ * take x*cos + rotate_half(x)*sin reading all R entries of the cos/sin row,
+ * dims >= R are copied; each product and the sum are rounded to the promoted
+ * dtype of (keys, cos) and the result to the storage type, exactly as PyTorch
+ * evaluates it.  rope_dtype is DVATTN_F32 or dtype (the model dtype the
+ * transformers rotary embedding returns).  Tokens whose position is negative
+ * (masked), past the block_tables row or on a page outside [0, num_blocks) are
+ * not written.  Uses shape fields W, Hkv, S, E, Ev, block_size,
+ * max_blocks_per_seq, num_blocks, rotary_dim; positions [W,S] and block_tables
+ * [W,max_blocks_per_seq] are contiguous int32; the other tensors are described
+ * by element strides (last dim contiguous; cos/sin strides may be 0 to
+ * broadcast one row, which makes this merge_caches' constant-offset
+ * re-rotation, attention.py:245-251).  Keys/values must not overlap the caches.
+ * Replaces attention.py:304 (key rotation) + attention.py:141-152 (append to the
+ * sequence's cache, transformers Cache.update). */
+typedef struct dvattn_kv_layout {
+    long long key_strides[3];     /* keys [W,Hkv,S,E]: strides of w, h, s */
+    long long value_strides[3];   /* values [W,Hkv,S,Ev] */
+    long long rope_strides[2];    /* cosines / sines [W,S,R]: strides of w, s */
+    long long k_cache_strides[3]; /* k_cache [num_blocks,block_size,Hkv,E]: page, row, head */
+    long long v_cache_strides[3]; /* v_cache [num_blocks,block_size,Hkv,Ev] */
+} dvattn_kv_layout;
+
+DVATTN_API dvattn_status dvattn_paged_kv_append(int dtype, int rope_dtype, void* k_cache, void* v_cache,
+                                     const int* block_tables, const int* positions, const void* keys,
+                                     const void* values, const void* cosines, const void* sines,
+                                     const dvattn_shape* shape, const dvattn_kv_layout* layout, void* stream);
+
+/* ---- per-view locations and rotary cos/sin on the device ---------------------
+ * locations [F,W,S] i32, cosines/sines [F,W,S,R] f32 (R = rotary_dim, full
+ * width, both halves equal) from fragment_lengths [F] i32 (device; lengths
+ * already including the S new tokens), order [W,F] i32 (order[w, j]: the view
+ * index of sequence w's j-th segment, its own segment last) and inv_freq
+ * [R/2] f32 (the model's rotary inverse frequencies):
+ *   locations[f,w,s] = (sum of the lengths of w's segments from f's place in
+ *                       its order to the end) - S + s
+ *   cos/sin[f,w,s,i] = cos/sin(float(locations[f,w,s]) * inv_freq[i % (R/2)])
+ *                      * attention_scaling
+ * A view missing from a sequence's order gets location -1 and cos 1, sin 0.
+ * round_dtype (-1, DVATTN_F16 or DVATTN_BF16) rounds cos/sin through that type,
+ * as the reference does when the model runs in it (rotary output in the model
+ * dtype, then .to(float)).
+ * Replaces attention.py:158-186 (DVAttnCache.update's host loops and the
+ * transformers rotary embedding call). */
+DVATTN_API dvattn_status dvattn_view_metadata(int* locations, float* cosines, float* sines,
+                                   const int* fragment_lengths, const int* order, const float* inv_freq,
+                                   float attention_scaling, int round_dtype, int F, int W, int S,
+                                   int rotary_dim, void* stream);
 
 #ifdef __cplusplus
 }

@@ -25,6 +25,14 @@ repository root) whose behaviour it restates:
 * ``contig_sdpa``     -- src/binding.cu:79-149 + kernel_v21.cuh:84-114
                          (per-view contiguous fragments ``[B, Hkv, L, E]``).
 * ``fused``           -- src/binding.cu:356-372 (rope, then contiguous sdpa).
+* ``apply_rotary``    -- python/dvattn/attention.py:75-88 (``rotate_half`` /
+                         ``apply_rotary_pos_emb``, the key-side rotation) as
+                         PyTorch evaluates it in the input dtypes.
+* ``kv_append``       -- attention.py:304 (key rotation) + 141-152 (append to the
+                         sequence's own cache) + 245-251 (merge_caches), on a
+                         paged cache.
+* ``view_metadata``   -- attention.py:158-186 (per-view locations from the
+                         segment orders, then the transformers rotary embedding).
 
 Pins (see tests/test_oracle.py): the rotation is checked against the
 reference's own ``rope_cpu`` (src/q_rope.h:3-35, compiled into ``oracle/_ref``
@@ -34,6 +42,11 @@ when the reference tree is present) and against transformers' Qwen2
 view/offset semantics against the dynamic-view identity (relative query
 rotation == absolute-position causal attention); page-table and varlen indexing
 against exact special cases (single visible key, uniform weights, id-coded V).
+The key-side rotation is checked against transformers' Qwen2
+``apply_rotary_pos_emb`` (bit for bit) and closed forms (identity, quarter
+turn, float64 rotation); the append against pages built from a known
+permutation; the view metadata against hand-computed locations and
+transformers' ``Qwen2RotaryEmbedding``.
 """
 from __future__ import annotations
 
@@ -49,6 +62,9 @@ __all__ = [
     "contig_sdpa",
     "fused",
     "varlen_token_to_seq",
+    "apply_rotary",
+    "kv_append",
+    "view_metadata",
 ]
 
 
@@ -274,3 +290,95 @@ def fused(scale: float, locations: torch.Tensor, queries: torch.Tensor, fragment
     """``dvattn_fused`` (binding.cu:356-372): returns (fp32 out, rotated queries)."""
     rq = rope_q(queries, cosines, sines)
     return contig_sdpa(scale, locations, rq, fragment_lengths, key_fragments, value_fragments), rq
+
+
+def apply_rotary(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Partial RoPE of the last dim as attention.py:82-88 computes it: dims
+    ``< R = cos.shape[-1]`` become ``x*cos + rotate_half(x)*sin`` (rotate_half =
+    ``cat(-x2, x1)``, attention.py:75-79), the rest pass through; every operation
+    in PyTorch's dtype promotion of (x, cos), the result cast back to x's dtype.
+    cos/sin broadcast against ``x[..., :R]``."""
+    R = cos.shape[-1]
+    x_rot, x_pass = x[..., :R], x[..., R:]
+    h = R // 2
+    rh = torch.cat((-x_rot[..., h:], x_rot[..., :h]), dim=-1)
+    emb = (x_rot * cos) + (rh * sin)
+    return torch.cat((emb, x_pass.to(emb.dtype)), dim=-1).to(x.dtype)
+
+
+def kv_append(k_cache: torch.Tensor, v_cache: torch.Tensor, block_tables: torch.Tensor, positions: torch.Tensor,
+              keys: torch.Tensor, values: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor):
+    """Write rotated keys and values of new tokens into a paged cache; returns
+    updated copies (CPU).
+
+    keys/values ``[W,Hkv,S,E]``; positions ``[W,S]``: logical position ``p`` of
+    token (w, s) in sequence w's token stream, stored at page
+    ``block_tables[w, p // bs]``, row ``p % bs`` of ``[P,bs,Hkv,E]`` caches (the
+    layout of the paged operators, binding.cu:194-196; paged_kernel_v21.cuh:102-120);
+    ``p < 0`` (a masked token, attention.py:141-147 copies only unmasked ones), a
+    logical page past the table row or a page outside ``[0, P)`` is not written.
+    cos/sin ``[W|1, S|1, R]``: the rotation of attention.py:304 at that token.
+    """
+    k = k_cache.clone()
+    v = v_cache.clone()
+    W, Hkv, S, E = keys.shape
+    P, bs = k.shape[0], k.shape[1]
+    maxB = block_tables.shape[1]
+    R = cos.shape[-1]
+    cb = cos.expand(W, S, R)
+    sb = sin.expand(W, S, R)
+    for w in range(W):
+        for s in range(S):
+            p = int(positions[w, s])
+            if p < 0:
+                continue
+            lp, row = divmod(p, bs)
+            if lp >= maxB:
+                continue
+            page = int(block_tables[w, lp])
+            if page < 0 or page >= P:
+                continue
+            k[page, row] = apply_rotary(keys[w, :, s, :], cb[w, s], sb[w, s])
+            v[page, row] = values[w, :, s, :]
+    return k, v
+
+
+def view_metadata(fragment_lengths, order, S: int, inv_freq: torch.Tensor, attention_scaling: float = 1.0,
+                  round_to=None):
+    """Per-view locations and cos/sin of a decode step (attention.py:158-186).
+
+    For each sequence w the reference walks its segment list backwards,
+    accumulating lengths (which already include the S new tokens), and gives the
+    segment at which it stands the locations ``arange(pos - S, pos)``
+    (attention.py:167-176).  cos/sin are transformers' default rotary embedding at
+    those positions: ``angle = float(position) * inv_freq`` (a K=1 fp32 matmul),
+    ``emb = cat(angle, angle)``, ``cos(emb) * scaling`` (and sin), returned in the
+    model dtype and converted to float32 (attention.py:181-184; ``round_to`` is
+    that model dtype).  A view absent from a sequence's order has no location in
+    the reference (it fails); here it gets -1 and the identity rotation.
+    """
+    fl = [int(x) for x in fragment_lengths]
+    F = len(fl)
+    W = len(order)
+    loc = torch.full((F, W, S), -1, dtype=torch.int32)
+    present = torch.zeros((F, W), dtype=torch.bool)
+    for w in range(W):
+        pos = 0
+        for g in reversed([int(x) for x in order[w]]):
+            pos += fl[g]
+            loc[g, w] = torch.arange(pos - S, pos, dtype=torch.int32)
+            present[g, w] = True
+    R = 2 * inv_freq.numel()
+    ang = loc.reshape(F * W, S).float()[:, :, None] * inv_freq.float()[None, None, :]
+    emb = torch.cat((ang, ang), dim=-1)
+    cos = emb.cos() * attention_scaling
+    sin = emb.sin() * attention_scaling
+    if round_to is not None:
+        cos = cos.to(round_to).float()
+        sin = sin.to(round_to).float()
+    cos = cos.reshape(F, W, S, R)
+    sin = sin.reshape(F, W, S, R)
+    miss = ~present
+    cos[miss] = 1.0
+    sin[miss] = 0.0
+    return loc, cos, sin

@@ -363,3 +363,123 @@ def test_golden_fixtures():
             rq = (O.rope_q if kind == "paged" else O.rope_q_varlen)(
                 torch.from_numpy(z["queries"]).to(dt), torch.from_numpy(z["cosines"]), torch.from_numpy(z["sines"]))
             assert np.array_equal(rq.float().numpy(), z[rq_name]), fn
+
+
+# ------------------------------------------------- K-side append, view metadata --
+
+def _rand(shape, dt):
+    return torch.randn(shape).to(dt)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("cos_dt", ["f32", "model"])
+@pytest.mark.parametrize("R", [128, 64])
+def test_key_rotation_matches_transformers_qwen2(dt, cos_dt, R):
+    """attention.py:82-88 (oracle apply_rotary) against transformers' Qwen2
+    apply_rotary_pos_emb on the rotated block, bit for bit, in the dtypes
+    PyTorch promotes to (model dtype cos/sin: every op rounded to it)."""
+    from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
+    W, H, S, E = 2, 3, 5, 128
+    k = _rand((W, H, S, E), dt)
+    c, s = hf_cs(RNG.integers(0, 200000, size=(W, S)), R)
+    if cos_dt == "model":
+        c, s = c.to(dt), s.to(dt)
+    ours = O.apply_rotary(k, c[:, None], s[:, None])
+    _, kr = apply_rotary_pos_emb(k[..., :R], k[..., :R], c, s, unsqueeze_dim=1)
+    assert torch.equal(ours[..., :R], kr.to(dt))
+    assert torch.equal(ours[..., R:], k[..., R:])
+    assert ours.dtype == dt
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_key_rotation_closed_forms(dt):
+    x = _rand((4, 128), dt)
+    R = 96
+    one, zero = torch.ones(R), torch.zeros(R)
+    assert torch.equal(O.apply_rotary(x, one, zero), x)                       # angle 0
+    q = O.apply_rotary(x, zero, one)                                          # quarter turn
+    assert torch.equal(q[:, :48], -x[:, 48:96]) and torch.equal(q[:, 48:96], x[:, :48])
+    assert torch.equal(q[:, 96:], x[:, 96:])
+    assert torch.equal(O.apply_rotary(x, torch.zeros(0), torch.zeros(0)), x)  # R = 0
+    # float64 rotation of each (e, e + R/2) pair by its angle
+    th = torch.from_numpy(RNG.uniform(-7, 7, size=R // 2))
+    c = torch.cat([th.cos(), th.cos()]).float()
+    s = torch.cat([th.sin(), th.sin()]).float()
+    y = O.apply_rotary(x.float(), c, s).double()
+    xd = x.double()
+    a, b = xd[:, :R // 2], xd[:, R // 2:R]
+    want = torch.cat([a * th.cos() - b * th.sin(), b * th.cos() + a * th.sin(), xd[:, R:]], 1)
+    assert torch.allclose(y, want, atol=1e-5, rtol=1e-5)
+
+
+def test_kv_append_oracle_places_tokens_by_page_table():
+    """Logical position p of sequence w lands in page bt[w, p // bs], row p % bs;
+    pages come from a known permutation, so the expected cache is built
+    independently; masked and out-of-table tokens leave the sentinel."""
+    W, Hkv, S, E, bs, maxB = 3, 2, 4, 16, 4, 3
+    P = W * maxB + 2
+    perm = torch.from_numpy(RNG.permutation(P)[: W * maxB].astype(np.int32)).reshape(W, maxB)
+    pos = torch.tensor([[0, 5, 11, -1], [3, 4, 7, 12], [1, 2, 9, 10]], dtype=torch.int32)  # 12: past the table
+    keys = torch.arange(W * Hkv * S * E, dtype=torch.float32).reshape(W, Hkv, S, E)
+    vals = -keys
+    kc = torch.full((P, bs, Hkv, E), 7.0)
+    vc = torch.full((P, bs, Hkv, E), 7.0)
+    one = torch.ones(1, 1, 0)
+    k2, v2 = O.kv_append(kc, vc, perm, pos, keys, vals, one, one)
+    want_k = kc.clone()
+    want_v = vc.clone()
+    for w in range(W):
+        for s in range(S):
+            p = int(pos[w, s])
+            if p < 0 or p >= maxB * bs:
+                continue
+            page = int(perm[w][p // bs])
+            want_k[page, p % bs] = keys[w, :, s]
+            want_v[page, p % bs] = vals[w, :, s]
+    assert torch.equal(k2, want_k) and torch.equal(v2, want_v)
+    assert int((k2 != 7.0).any(-1).any(-1).sum()) == 10  # ten tokens written
+
+
+def test_kv_append_merge_is_rotation_additive():
+    """merge_caches re-rotates keys already rotated at position a by the target
+    length b (attention.py:245-251): the result is the rotation at a + b
+    (fp32, to rounding)."""
+    E, R = 128, 128
+    k = torch.randn(3, E)
+    a, b = 1234, 40000
+    ca, sa = hf_cs([a], R)
+    cb, sb = hf_cs([b], R)
+    cab, sab = hf_cs([a + b], R)
+    twice = O.apply_rotary(O.apply_rotary(k, ca[0], sa[0]), cb[0], sb[0])
+    once = O.apply_rotary(k, cab[0], sab[0])
+    assert torch.allclose(twice, once, atol=2e-5)
+
+
+def test_view_metadata_hand_computed_locations():
+    # lengths [5, 3, 4]; sequence 0 orders its segments 0,1,2 and sequence 1 2,0,1
+    loc, cos, sin = O.view_metadata([5, 3, 4], [[0, 1, 2], [2, 0, 1]], 2, torch.tensor([1.0, 0.25]))
+    want = torch.tensor([[[10, 11], [6, 7]], [[5, 6], [1, 2]], [[2, 3], [10, 11]]], dtype=torch.int32)
+    assert torch.equal(loc, want)
+    assert torch.equal(cos[..., :2], cos[..., 2:])
+    assert cos[0, 0, 0, 0].item() == np.float32(np.cos(np.float32(10.0)))
+    # a segment missing from a sequence's order: location -1, identity rotation
+    loc, cos, sin = O.view_metadata([4, 4], [[0, 1], [1, 1]], 1, torch.tensor([0.5]))
+    assert loc[0, 1, 0].item() == -1 and cos[0, 1, 0, 0].item() == 1.0 and sin[0, 1, 0, 0].item() == 0.0
+    assert loc[1, 1, 0].item() == 7  # first place of a repeated segment wins (the backward walk assigns it last)
+
+
+@pytest.mark.parametrize("round_to", [None, torch.bfloat16])
+def test_view_metadata_cos_sin_match_transformers_rotary(round_to):
+    from transformers import Qwen2Config
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RotaryEmbedding
+    cfg = Qwen2Config(hidden_size=256, num_attention_heads=2, num_key_value_heads=1, head_dim=128,
+                      rope_theta=500000.0, max_position_embeddings=1 << 20)
+    rot = Qwen2RotaryEmbedding(cfg)
+    lens = [70000, 33, 900]
+    order = [[0, 1, 2], [1, 2, 0], [2, 0, 1], [0, 2, 1]]
+    S = 3
+    loc, cos, sin = O.view_metadata(lens, order, S, rot.inv_freq, 1.0, round_to)
+    x = torch.zeros(1, dtype=round_to or torch.float32)
+    c_ref, s_ref = rot(x, loc.reshape(-1, S).long())
+    assert torch.equal(cos, c_ref.float().reshape(cos.shape))
+    assert torch.equal(sin, s_ref.float().reshape(sin.shape))
