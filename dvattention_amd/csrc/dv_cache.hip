@@ -81,57 +81,53 @@ __device__ inline float rope_elem(float x, float xp, float c, float s, bool firs
 // position is negative, past the block table row or on an invalid page are not
 // written.
 template <int DT, int CDT, int RUN>
-__global__ __launch_bounds__(256) void dv_kv_append(const AppendParams p, long long nruns, int runs) {
+__global__ __launch_bounds__(256) void dv_kv_append(const AppendParams p, uint32_t nruns, uint32_t runs) {
     using raw = typename Tr<DT>::raw;
     using craw = typename Tr<CDT>::raw;
-    const long long idx = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    // 32-bit index arithmetic: the launcher keeps a launch below 2^31 runs
+    const uint32_t idx = blockIdx.x * 256u + threadIdx.x;
     if (idx >= nruns) return;
-    const long long hr = idx / runs;
+    const uint32_t hr = idx / runs;
     const int d0 = (int)(idx - hr * runs) * RUN;
-    const int h = (int)(hr % p.Hkv);
-    const long long n = hr / p.Hkv;  // token index w*S + s
-    const int w = (int)(n / p.S);
-    const int s = (int)(n - (long long)w * p.S);
+    const uint32_t n = hr / (uint32_t)p.Hkv;  // token index w*S + s
+    const int h = (int)(hr - n * (uint32_t)p.Hkv);
+    const int w = (int)(n / (uint32_t)p.S);
+    const int s = (int)(n - (uint32_t)w * (uint32_t)p.S);
+    // the token's inputs are loaded first, then the page lookup (positions,
+    // then block_tables: two dependent loads) runs while they are in flight
     const int ps = p.pos[n];
+    const bool has_k = d0 < p.E, has_v = d0 < p.Ev;
+    const bool rot = has_k && d0 < p.R;
+    const int half = p.R >> 1;
+    const bool first = d0 < half;  // a rotated run lies within one half (R/2 % RUN == 0)
+    raw xa[RUN], xb[RUN], vo[RUN];
+    craw c[RUN], sn[RUN];
+    if (has_k) {
+        const raw* x = reinterpret_cast<const raw*>(p.k) + w * p.ks[0] + h * p.ks[1] + s * p.ks[2];
+        load_run<raw, RUN>(x + d0, xa);
+        if (rot) {
+            const long long co = w * p.cs[0] + s * p.cs[1] + d0;
+            load_run<raw, RUN>(x + (first ? d0 + half : d0 - half), xb);
+            load_run<craw, RUN>(reinterpret_cast<const craw*>(p.cosv) + co, c);
+            load_run<craw, RUN>(reinterpret_cast<const craw*>(p.sinv) + co, sn);
+        }
+    }
+    if (has_v)
+        load_run<raw, RUN>(reinterpret_cast<const raw*>(p.v) + w * p.vs[0] + h * p.vs[1] + s * p.vs[2] + d0, vo);
     if (ps < 0) return;
     const int lp = ps / p.bs;
     if (lp >= p.maxB) return;
     const int page = p.bt[(long long)w * p.maxB + lp];
+    if (has_k && rot) {
+#pragma unroll
+        for (int e = 0; e < RUN; ++e)
+            xa[e] = Tr<DT>::fromf(rope_elem<DT, CDT>(Tr<DT>::tof(xa[e]), Tr<DT>::tof(xb[e]), Tr<CDT>::tof(c[e]),
+                                                     Tr<CDT>::tof(sn[e]), first));
+    }
     if (page < 0 || page >= p.nblocks) return;
     const long long row = ps - (long long)lp * p.bs;
-
-    if (d0 < p.E) {
-        const raw* x = reinterpret_cast<const raw*>(p.k) + w * p.ks[0] + h * p.ks[1] + s * p.ks[2];
-        raw o[RUN];
-        if (d0 >= p.R) {
-            load_run<raw, RUN>(x + d0, o);
-        } else {
-            // a run lies within one half of the rotary block (R/2 % RUN == 0)
-            const int half = p.R >> 1;
-            const bool first = d0 < half;
-            const int pd = first ? d0 + half : d0 - half;
-            const long long co = w * p.cs[0] + s * p.cs[1] + d0;
-            raw xa[RUN], xb[RUN];
-            craw c[RUN], sn[RUN];
-            load_run<raw, RUN>(x + d0, xa);
-            load_run<raw, RUN>(x + pd, xb);
-            load_run<craw, RUN>(reinterpret_cast<const craw*>(p.cosv) + co, c);
-            load_run<craw, RUN>(reinterpret_cast<const craw*>(p.sinv) + co, sn);
-#pragma unroll
-            for (int e = 0; e < RUN; ++e)
-                o[e] = Tr<DT>::fromf(rope_elem<DT, CDT>(Tr<DT>::tof(xa[e]), Tr<DT>::tof(xb[e]), Tr<CDT>::tof(c[e]),
-                                                        Tr<CDT>::tof(sn[e]), first));
-        }
-        raw* dst = reinterpret_cast<raw*>(p.kc) + page * p.kcs[0] + row * p.kcs[1] + h * p.kcs[2] + d0;
-        store_run<raw, RUN>(dst, o);
-    }
-    if (d0 < p.Ev) {
-        const raw* v = reinterpret_cast<const raw*>(p.v) + w * p.vs[0] + h * p.vs[1] + s * p.vs[2] + d0;
-        raw o[RUN];
-        load_run<raw, RUN>(v, o);
-        raw* dst = reinterpret_cast<raw*>(p.vc) + page * p.vcs[0] + row * p.vcs[1] + h * p.vcs[2] + d0;
-        store_run<raw, RUN>(dst, o);
-    }
+    if (has_k) store_run<raw, RUN>(reinterpret_cast<raw*>(p.kc) + page * p.kcs[0] + row * p.kcs[1] + h * p.kcs[2] + d0, xa);
+    if (has_v) store_run<raw, RUN>(reinterpret_cast<raw*>(p.vc) + page * p.vcs[0] + row * p.vcs[1] + h * p.vcs[2] + d0, vo);
 }
 
 template <int DT, int CDT, int RUN>
@@ -140,8 +136,10 @@ hipError_t append_go(const AppendParams& p, hipStream_t stream) {
     const int runs = (E + RUN - 1) / RUN;
     const long long nruns = (long long)p.W * p.S * p.Hkv * runs;
     if (nruns == 0) return hipSuccess;
+    if (nruns >= (1ll << 31)) return hipErrorInvalidValue;  // the C ABI rejects such calls first
     const long long blocks = (nruns + 255) / 256;
-    hipLaunchKernelGGL((dv_kv_append<DT, CDT, RUN>), dim3((unsigned)blocks), dim3(256), 0, stream, p, nruns, runs);
+    hipLaunchKernelGGL((dv_kv_append<DT, CDT, RUN>), dim3((unsigned)blocks), dim3(256), 0, stream, p,
+                       (uint32_t)nruns, (uint32_t)runs);
     return hipGetLastError();
 }
 

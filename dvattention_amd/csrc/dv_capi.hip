@@ -395,6 +395,10 @@ dvattn_status dvattn_paged_kv_append(int dtype, int rope_dtype, void* k_cache, v
     if (s->block_size <= 0) return fail(DVATTN_ERR_INVALID, "block_size must be positive (got %d)", s->block_size);
     if (s->max_blocks_per_seq < 0 || s->num_blocks < 0)
         return fail(DVATTN_ERR_INVALID, "max_blocks_per_seq / num_blocks must be >= 0");
+    // the kernel indexes (token, head, element) in 32 bits
+    if ((long long)s->W * s->S * s->Hkv * (s->E > s->Ev ? s->E : s->Ev) >= (1ll << 31))
+        return fail(DVATTN_ERR_UNSUPPORTED, "%lld key elements in one call exceed 2^31",
+                    (long long)s->W * s->S * s->Hkv * (s->E > s->Ev ? s->E : s->Ev));
     if (!k_cache || !v_cache || !keys || !values || !positions || (s->max_blocks_per_seq > 0 && !block_tables) ||
         (s->rotary_dim > 0 && (!cosines || !sines)))
         return fail(DVATTN_ERR_INVALID, "null pointer");

@@ -162,3 +162,47 @@ def test_python_api_mirrors_reference_names():
     s = torch.randn(2, 4, 6)
     y = A.apply_rotary_pos_emb(x, c, s)
     assert torch.equal(y[..., 6:], x[..., 6:])
+
+
+def _kv_shape(**kw):
+    from dvattention_amd import capi
+    d = dict(F=0, W=2, Hq=0, Hkv=8, E=128, Ev=128, S=4, block_size=16, max_blocks_per_seq=4, total_q_tokens=0,
+             num_blocks=8, rotary_dim=128)
+    d.update(kw)
+    return capi.Shape(**d)
+
+
+@pytest.mark.parametrize("kw,rope_dt,status,needle", [
+    (dict(W=1 << 16, S=4096), 0, 2, "2^31"),     # 32-bit element indexing
+    (dict(), 1, 2, "cos/sin dtype"),             # f16 cos/sin for a bf16 cache
+    (dict(rotary_dim=7), 0, 2, "rotary_dim"),
+    (dict(rotary_dim=256), 0, 2, "rotary_dim"),  # R > E
+    (dict(block_size=0), 0, 1, "block_size"),
+    (dict(S=-1), 0, 1, "negative"),
+])
+def test_kv_append_validation(kw, rope_dt, status, needle):
+    from dvattention_amd import capi
+    L = capi.lib()
+    p = ctypes.c_void_p(0x1000)
+    s = _kv_shape(**kw)
+    lay = capi.KvLayout()
+    st = L.dvattn_paged_kv_append(2, rope_dt, p, p, p, p, p, p, p, p, ctypes.byref(s), ctypes.byref(lay), None)
+    assert st == status and needle in L.dvattn_last_error().decode()
+
+
+def test_kv_append_and_metadata_null_and_empty():
+    from dvattention_amd import capi
+    L = capi.lib()
+    p = ctypes.c_void_p(0x1000)
+    lay = capi.KvLayout()
+    s = _kv_shape()
+    assert L.dvattn_paged_kv_append(2, 0, p, None, p, p, p, p, p, p, ctypes.byref(s), ctypes.byref(lay), None) == 1
+    s = _kv_shape(W=0)
+    assert L.dvattn_paged_kv_append(2, 0, None, None, None, None, None, None, None, None, ctypes.byref(s),
+                                    ctypes.byref(lay), None) == 0
+    # view metadata: odd rotary dim, unknown rounding dtype, null pointers, empty
+    assert L.dvattn_view_metadata(p, p, p, p, p, p, 1.0, -1, 2, 3, 1, 63, None) == 2
+    assert L.dvattn_view_metadata(p, p, p, p, p, p, 1.0, 7, 2, 3, 1, 64, None) == 2
+    assert L.dvattn_view_metadata(p, None, p, p, p, p, 1.0, -1, 2, 3, 1, 64, None) == 1
+    assert L.dvattn_view_metadata(p, p, p, p, p, p, 1.0, -1, -1, 3, 1, 64, None) == 1
+    assert L.dvattn_view_metadata(None, None, None, None, None, None, 1.0, -1, 0, 3, 1, 64, None) == 0
