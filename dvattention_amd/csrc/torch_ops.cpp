@@ -434,7 +434,9 @@ void dvattn_fused_op(at::Tensor& out, at::Tensor& rq, double scale, const at::Te
 // The K side of a decode step (attention.py:304 rotation + 141-152 cache append)
 // and merge_caches' re-rotation (attention.py:245-251) on a paged cache.
 // keys/values [W,Hkv,S,E|Ev] and the caches may be strided views (last dim
-// contiguous); cos/sin [W|1, S|1, R] broadcast over size-1 dims.
+// contiguous); cos/sin [W|1, S|1, R] broadcast over size-1 dims.  Keys/values
+// may live in the cache tensors (merge_caches between segments of one pool) but
+// must not overlap the rows being written.
 void dvattn_paged_kv_append_op(at::Tensor& k_cache, at::Tensor& v_cache, const at::Tensor& block_tables,
                                const at::Tensor& positions, const at::Tensor& keys, const at::Tensor& values,
                                const at::Tensor& cosines, const at::Tensor& sines) {
@@ -467,9 +469,6 @@ void dvattn_paged_kv_append_op(at::Tensor& k_cache, at::Tensor& v_cache, const a
     for (int i : {6, 7})
         TORCH_CHECK(all[i]->size(2) <= 1 || all[i]->stride(2) == 1, "dvattn_paged_kv_append: the last dim of ",
                     names[i], " must be contiguous");
-    TORCH_CHECK(!keys.is_alias_of(k_cache) && !values.is_alias_of(v_cache) && !keys.is_alias_of(v_cache) &&
-                    !values.is_alias_of(k_cache),
-                "dvattn_paged_kv_append: keys/values must not share storage with the caches");
     const int64_t W = keys.size(0), Hkv = keys.size(1), S = keys.size(2), E = keys.size(3);
     const int64_t Ev = values.size(3);
     TORCH_CHECK(values.size(0) == W && values.size(1) == Hkv && values.size(2) == S,

@@ -1,0 +1,308 @@
+"""Transformers integration of the DVAttn decode path: ``DVAttnCache``,
+``AttentionModule`` and ``model_surgery`` of the reference
+(python/dvattn/attention.py:100-343), for transformers 5, over this package's
+HIP operators.
+
+What changes against the reference, and why:
+
+* Segments (the reference's per-worker HF caches, attention.py:109-119) live in
+  one preallocated pool per layer, ``[num_segments, Hkv, capacity, E]`` for K and
+  for V, instead of tensors that ``torch.cat`` regrows every step.  A segment is
+  a slice of the pool; the attention op reads it in place (its
+  ``fragment_lengths`` bound the visible keys, so the unused capacity is never
+  read).
+* The K side of a step is one ``dvattn_paged_kv_append`` launch for all workers:
+  key rotation (attention.py:304) fused with the write into each worker's
+  segment (attention.py:141-152), the pool seen as ``[segments, capacity, Hkv,
+  E]`` pages of ``capacity`` tokens.
+* Locations and query cos/sin (attention.py:158-186) come from one
+  ``dvattn_view_metadata`` launch per step; the host only uploads the segment
+  lengths and orders.
+* The attention is ``dvattn_fused`` as in the reference's non-eager path
+  (attention.py:319-331).
+
+The three device operations are reached through an ``ops`` object (default:
+this package's HIP operators), so the module code can also be driven by a
+checker implementation in tests.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Dict, List, Optional
+
+import torch
+from torch import nn
+
+from . import attention as _A
+
+
+class HipOps:
+    """The device operations of a decode step (this package's HIP operators)."""
+
+    @staticmethod
+    def kv_append(keys, values, positions, cos, sin, k_pages, v_pages, block_tables):
+        _A.dvattn_paged_kv_append(keys, values, positions, cos, sin, k_pages, v_pages, block_tables)
+
+    @staticmethod
+    def view_metadata(fragment_lengths, order, S, inv_freq, attention_scaling, round_to):
+        return _A.dvattn_view_metadata(fragment_lengths, order, S, inv_freq, attention_scaling, round_to)
+
+    @staticmethod
+    def fused(queries, locations, keys, values, scale, fragment_lengths, cosines, sines, rotated_queries, out):
+        return _A.dvattn_fused(queries, locations, keys, values, scale, fragment_lengths, cosines, sines,
+                               rotated_queries=rotated_queries, out=out)
+
+
+@dataclass
+class CacheStructure:
+    """What the attention of one layer needs (attention.py:100-106)."""
+    keys: list       # per view: [1, Hkv, capacity, E]
+    values: list
+    frags: torch.Tensor  # fragment_lengths [F] int32
+    cos: torch.Tensor    # [F, W, S, R] float32
+    sin: torch.Tensor
+    loc: torch.Tensor    # [F, W, S] int32
+
+
+class SegmentPool:
+    """Preallocated K/V storage for ``num_segments`` segments of every layer."""
+
+    def __init__(self, config, num_segments: int, capacity: int, dtype: torch.dtype, device):
+        self.num_layers = config.num_hidden_layers
+        self.Hkv = config.num_key_value_heads
+        self.E = getattr(config, "head_dim", None) or config.hidden_size // config.num_attention_heads
+        self.capacity = capacity
+        shape = (num_segments, self.Hkv, capacity, self.E)
+        self.k = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(self.num_layers)]
+        self.v = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(self.num_layers)]
+        self.segments = [Segment(self, i) for i in range(num_segments)]
+
+    def __getitem__(self, i: int) -> "Segment":
+        return self.segments[i]
+
+
+class Segment:
+    """One segment (a contiguous run of tokens shared by the workers that see
+    it); stands in for the reference's per-segment HF cache."""
+
+    def __init__(self, pool: SegmentPool, index: int):
+        self.pool = pool
+        self.index = index
+        self.lengths = [0] * pool.num_layers
+
+    def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
+        return self.lengths[layer_idx or 0]
+
+    def keys(self, layer_idx: int) -> torch.Tensor:
+        return self.pool.k[layer_idx][self.index:self.index + 1]
+
+    def values(self, layer_idx: int) -> torch.Tensor:
+        return self.pool.v[layer_idx][self.index:self.index + 1]
+
+
+class DVAttnCache:
+    """Multi-worker dynamic-view cache (attention.py:109-239).
+
+    ``cache_structure[w]`` lists the segments worker w attends to, in its own
+    order (its own segment, where its new tokens go, last by default:
+    ``write_to``).  All segments must come from one ``SegmentPool``.  Unlike the
+    reference, a worker may leave out segments other workers list; it does not
+    see them.
+    """
+
+    def __init__(self, cache_structure: List[List[Segment]], model, write_to: Optional[List[Segment]] = None,
+                 ops=HipOps):
+        self.model = model.model
+        self.cache_structure = cache_structure
+        self.write_to = write_to if write_to else [cl[-1] for cl in cache_structure]
+        self.pool = cache_structure[0][0].pool
+        self.ops = ops
+        self.cosines = None
+        self.sines = None
+        self.locations = None
+        self.segments: List[Segment] = []
+        self.frags = None
+        self.queries_buffer = None
+        self.att_buffer = None
+        self._positions = None
+        self._wt_table = None
+
+    def get_seq_length(self, layer_idx: Optional[int] = 0) -> int:
+        return self.cache_structure[0][-1].get_seq_length(layer_idx)
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int,
+               cache_kwargs: Optional[Dict[str, Any]] = None) -> CacheStructure:
+        """Rotate and append the new keys/values of every worker into its
+        ``write_to`` segment, then (layer 0) rebuild the view metadata.
+
+        key_states: ``[W, Hkv, S, E]`` *before* rotation (the reference rotates
+        at attention.py:304 and appends at :141-152; here both are one launch);
+        cache_kwargs: ``cos``/``sin`` (the model's position embeddings ``[W, S,
+        R]``) and an optional left-padding ``mask`` ``[W, S]``.
+        """
+        W, _, S, _ = key_states.shape
+        assert W == len(self.cache_structure)
+        dev = key_states.device
+        mask = cache_kwargs.get("mask") if cache_kwargs else None
+        if layer_idx == 0:
+            # positions of the new tokens in each worker's segment (left padding -> -1),
+            # shared by all layers of this step
+            n_new = mask.sum(dim=1).tolist() if mask is not None else [S] * W
+            pos = torch.full((W, S), -1, dtype=torch.int32)
+            for w in range(W):
+                n = int(n_new[w])
+                base = self.write_to[w].get_seq_length(0)
+                if base + n > self.pool.capacity:
+                    raise RuntimeError(f"segment {self.write_to[w].index} is full ({base} + {n} > "
+                                       f"{self.pool.capacity} tokens)")
+                pos[w, S - n:] = torch.arange(base, base + n, dtype=torch.int32)
+            self._n_new = [int(n) for n in n_new]
+            self._positions = pos.to(dev, non_blocking=True)
+            self._wt_table = torch.tensor([[seg.index] for seg in self.write_to], dtype=torch.int32).to(dev)
+        cos, sin = cache_kwargs["cos"], cache_kwargs["sin"]
+        pages_k = self.pool.k[layer_idx].permute(0, 2, 1, 3)  # [segments, capacity, Hkv, E]
+        pages_v = self.pool.v[layer_idx].permute(0, 2, 1, 3)
+        self.ops.kv_append(key_states, value_states, self._positions, cos, sin, pages_k, pages_v, self._wt_table)
+        for w in range(W):
+            self.write_to[w].lengths[layer_idx] += self._n_new[w]
+
+        if layer_idx == 0:
+            # views in the order of worker 0's structure (attention.py:158-166), then
+            # any segment only other workers list; each worker's location for a view
+            # sums the lengths from that view to the end of its own order
+            # (attention.py:167-176).  A worker whose structure omits a view does
+            # not see it (location -1); the reference requires every worker to list
+            # every segment
+            segments = []
+            index = {}
+            for cl in self.cache_structure:
+                for seg in cl:
+                    if id(seg) not in index:
+                        index[id(seg)] = len(segments)
+                        segments.append(seg)
+            F = len(segments)
+            rows = [[-1] * (F - len(cl)) + [index[id(seg)] for seg in cl] for cl in self.cache_structure]
+            order = torch.tensor(rows, dtype=torch.int32).to(dev)
+            frags = torch.tensor([seg.get_seq_length(0) for seg in segments], dtype=torch.int32).to(dev)
+            # inv_freq as the rotary embedding uses it (a model cast to a 16-bit dtype
+            # rounds the buffer; transformers converts it back to float32)
+            rot = self.model.rotary_emb
+            round_to = key_states.dtype if key_states.dtype != torch.float32 else None
+            self.locations, self.cosines, self.sines = self.ops.view_metadata(
+                frags, order, S, rot.inv_freq.float(), float(rot.attention_scaling), round_to)
+            self.segments = segments
+            self.frags = frags
+        return CacheStructure(keys=[seg.keys(layer_idx) for seg in self.segments],
+                              values=[seg.values(layer_idx) for seg in self.segments],
+                              cos=self.cosines, sin=self.sines, loc=self.locations, frags=self.frags)
+
+    def get_queries_buffer(self, queries: torch.Tensor, layer_idx: int) -> torch.Tensor:
+        if layer_idx == 0:  # attention.py:194-199
+            self.queries_buffer = torch.empty((self.cosines.size(0),) + tuple(queries.shape), dtype=queries.dtype,
+                                              device=queries.device)
+        return self.queries_buffer
+
+    def get_att_buffer(self, r_queries: torch.Tensor, layer_idx: int) -> torch.Tensor:
+        if layer_idx == 0:  # attention.py:201-206
+            self.att_buffer = torch.empty(tuple(r_queries.shape[1:4]) + (self.pool.E,), dtype=r_queries.dtype,
+                                          device=r_queries.device)
+        return self.att_buffer
+
+    def get_input_kwargs(self, input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor] = None):
+        """Model inputs of one step (attention.py:208-236): per-worker position ids
+        continue each worker's own segment; the mask is handed to the layers as
+        is (transformers skips its own mask construction for a prepared dict)."""
+        nw = len(self.cache_structure)
+        assert input_ids.shape[0] == nw, (input_ids.shape, nw)
+        if attention_mask is not None:
+            new_tokens = attention_mask.sum(dim=1).tolist()
+        else:
+            new_tokens = [input_ids.shape[1]] * nw
+        pos_ids = []
+        for w in range(nw):
+            e = self.write_to[w].get_seq_length() + int(new_tokens[w])
+            pos_ids.append(torch.arange(e - input_ids.shape[1], e, dtype=torch.int64, device=input_ids.device))
+        return {
+            "input_ids": input_ids,
+            "attention_mask": {"full_attention": attention_mask},
+            "past_key_values": self,
+            "use_cache": True,
+            "position_ids": torch.stack(pos_ids, dim=0),
+        }
+
+
+def merge_caches(target: Segment, source: Segment, model, ops=HipOps) -> None:
+    """Append ``source`` to ``target`` with its keys re-rotated by the target's
+    length (attention.py:245-251): one append per layer with a single cos/sin row."""
+    assert target.pool is source.pool
+    pool = target.pool
+    rot = model.model.rotary_emb
+    L = source.get_seq_length(0)
+    dev = pool.k[0].device
+    for layer in range(pool.num_layers):
+        t0 = target.get_seq_length(layer)
+        if t0 + L > pool.capacity:
+            raise RuntimeError("merge_caches: target segment is full")
+        ref = pool.k[layer]
+        cos, sin = rot(ref, torch.full((1, 1), t0, dtype=torch.int64, device=dev))
+        pos = (t0 + torch.arange(L, dtype=torch.int32, device=dev)).reshape(1, L)
+        table = torch.tensor([[target.index]], dtype=torch.int32, device=dev)
+        ops.kv_append(source.keys(layer)[:, :, :L], source.values(layer)[:, :, :L], pos, cos.reshape(1, 1, -1),
+                      sin.reshape(1, 1, -1), pool.k[layer].permute(0, 2, 1, 3), pool.v[layer].permute(0, 2, 1, 3),
+                      table)
+        target.lengths[layer] += L
+
+
+class AttentionModule(nn.Module):
+    """Drop-in self-attention of a transformers decoder layer (attention.py:254-331)."""
+
+    def __init__(self, config, layer_idx: int):
+        super().__init__()
+        self.config = config
+        self.layer_idx = layer_idx
+        self.head_dim = getattr(config, "head_dim", None) or config.hidden_size // config.num_attention_heads
+        self.num_key_value_groups = config.num_attention_heads // config.num_key_value_heads
+        self.scaling = self.head_dim ** -0.5
+        self.attention_dropout = config.attention_dropout
+        self.is_causal = True
+        self.q_proj = nn.Linear(config.hidden_size, config.num_attention_heads * self.head_dim, bias=True)
+        self.k_proj = nn.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=True)
+        self.v_proj = nn.Linear(config.hidden_size, config.num_key_value_heads * self.head_dim, bias=True)
+        self.o_proj = nn.Linear(config.num_attention_heads * self.head_dim, config.hidden_size, bias=False)
+
+    def forward(self, hidden_states: torch.Tensor, position_embeddings=None, attention_mask=None,
+                past_key_values: Optional[DVAttnCache] = None, past_key_value: Optional[DVAttnCache] = None,
+                position_ids: Optional[torch.Tensor] = None, **kwargs):
+        cache_obj = past_key_values if past_key_values is not None else past_key_value
+        input_shape = hidden_states.shape[:-1]
+        hidden_shape = (*input_shape, -1, self.head_dim)
+        if input_shape[0] != 1:
+            assert position_ids is not None, "When processing multiple workers, `position_ids` are mandatory"
+        query_states = self.q_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        key_states = self.k_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        value_states = self.v_proj(hidden_states).view(hidden_shape).transpose(1, 2)
+        cos, sin = position_embeddings
+        # the key rotation (attention.py:304) happens inside the cache append
+        cache = cache_obj.update(key_states, value_states, self.layer_idx,
+                                 {"cos": cos, "sin": sin, "mask": attention_mask})
+        rq = cache_obj.get_queries_buffer(query_states, self.layer_idx)
+        out = cache_obj.get_att_buffer(rq, self.layer_idx)
+        cache_obj.ops.fused(query_states, cache.loc, cache.keys, cache.values, self.scaling, cache.frags, cache.cos,
+                            cache.sin, rq, out)
+        attn_output = out.transpose(1, 2).reshape(*input_shape, -1).contiguous()
+        return self.o_proj(attn_output), None
+
+
+def model_surgery(model) -> None:
+    """Swap every decoder layer's self-attention for ``AttentionModule``, keeping
+    its projection weights (attention.py:334-343).  Masks are handed through by
+    ``DVAttnCache.get_input_kwargs``."""
+    for layer in model.model.layers:
+        old = layer.self_attn
+        new = AttentionModule(model.model.config, old.layer_idx)
+        new.q_proj, new.k_proj, new.v_proj, new.o_proj = old.q_proj, old.k_proj, old.v_proj, old.o_proj
+        layer.self_attn = new
+
+
+__all__ = ["CacheStructure", "SegmentPool", "Segment", "DVAttnCache", "merge_caches", "AttentionModule",
+           "model_surgery", "HipOps"]

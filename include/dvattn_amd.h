@@ -183,7 +183,8 @@ DVATTN_API dvattn_status dvattn_varlen_rope(int dtype, void* out, const void* qu
  * [W,max_blocks_per_seq] are contiguous int32; the other tensors are described
  * by element strides (last dim contiguous; cos/sin strides may be 0 to
  * broadcast one row, which makes this merge_caches' constant-offset
- * re-rotation, attention.py:245-251).  Keys/values must not overlap the caches.
+ * re-rotation, attention.py:245-251).  Keys/values must not overlap the cache
+ * rows this call writes (they may live elsewhere in the cache allocations).
  * Replaces attention.py:304 (key rotation) + attention.py:141-152 (append to the
  * sequence's cache, transformers Cache.update). */
 typedef struct dvattn_kv_layout {

@@ -355,7 +355,8 @@ def view_metadata(fragment_lengths, order, S: int, inv_freq: torch.Tensor, atten
     ``emb = cat(angle, angle)``, ``cos(emb) * scaling`` (and sin), returned in the
     model dtype and converted to float32 (attention.py:181-184; ``round_to`` is
     that model dtype).  A view absent from a sequence's order has no location in
-    the reference (it fails); here it gets -1 and the identity rotation.
+    the reference (it fails); here it gets -1 and the identity rotation.  Order
+    entries outside ``[0, F)`` are padding and skipped.
     """
     fl = [int(x) for x in fragment_lengths]
     F = len(fl)
@@ -365,6 +366,8 @@ def view_metadata(fragment_lengths, order, S: int, inv_freq: torch.Tensor, atten
     for w in range(W):
         pos = 0
         for g in reversed([int(x) for x in order[w]]):
+            if not 0 <= g < F:
+                continue  # padding of a sequence that lists fewer views
             pos += fl[g]
             loc[g, w] = torch.arange(pos - S, pos, dtype=torch.int32)
             present[g, w] = True

@@ -238,8 +238,6 @@ def test_kv_append_rejects_bad_arguments(dv, gpu):
         dv.dvattn_paged_kv_append(keys, vals, pos, c.half(), s.half(), kc, vc, bt)
     with pytest.raises(RuntimeError, match="keys must have dtype"):
         dv.dvattn_paged_kv_append(keys.float(), vals, pos, c, s, kc, vc, bt)
-    with pytest.raises(RuntimeError, match="must not share storage"):
-        dv.dvattn_paged_kv_append(kc[:3, :5].permute(0, 2, 1, 3), vals, pos, c, s, kc, vc, bt)
     with pytest.raises(RuntimeError, match="even"):
         dv.dvattn_paged_kv_append(keys, vals, pos, c[..., :63], s[..., :63], kc, vc, bt)
 

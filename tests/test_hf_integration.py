@@ -1,0 +1,215 @@
+"""Model integration (dvattention_amd.hf: DVAttnCache / AttentionModule /
+model_surgery, python/dvattn/attention.py:100-343) on a random-init Qwen2 of
+transformers 5 (no checkpoint is available offline).
+
+Exact reductions pin the integration: with one view the dynamic-view decode is
+ordinary causal attention, and workers that see only a shared prompt plus their
+own tokens each decode like a single sequence -- both must match transformers'
+own eager attention on the concatenated tokens.  Workers that see each other's
+segments have no such reduction; there the HIP run is compared with the same
+module code driven by the CPU oracle.
+
+CPU tests drive the module code with the oracle ops (host logic of the
+integration); GPU tests use the HIP operators.
+"""
+import copy
+
+import pytest
+import torch
+
+from oracle import dvattn_oracle as O
+
+transformers = pytest.importorskip("transformers")
+
+
+class OracleOps:
+    """The three device operations of a decode step, computed by the CPU oracle."""
+
+    @staticmethod
+    def kv_append(keys, values, positions, cos, sin, k_pages, v_pages, block_tables):
+        k2, v2 = O.kv_append(k_pages.cpu(), v_pages.cpu(), block_tables.cpu(), positions.cpu(), keys.cpu(),
+                             values.cpu(), cos.cpu(), sin.cpu())
+        k_pages.copy_(k2)
+        v_pages.copy_(v2)
+
+    @staticmethod
+    def view_metadata(fragment_lengths, order, S, inv_freq, attention_scaling, round_to):
+        dev = fragment_lengths.device
+        loc, c, s = O.view_metadata(fragment_lengths.tolist(), order.tolist(), S, inv_freq.cpu(), attention_scaling,
+                                    round_to)
+        return loc.to(dev), c.to(dev), s.to(dev)
+
+    @staticmethod
+    def fused(queries, locations, keys, values, scale, fragment_lengths, cosines, sines, rotated_queries, out):
+        o, rq = O.fused(scale, locations.cpu(), queries.cpu(), fragment_lengths.cpu(), [k.cpu() for k in keys],
+                        [v.cpu() for v in values], cosines.cpu(), sines.cpu())
+        rotated_queries.copy_(rq)
+        out.copy_(o.to(out.dtype))
+        return out
+
+
+def tiny_qwen2(dtype, device, seed=0):
+    from transformers import Qwen2Config, Qwen2ForCausalLM
+    cfg = Qwen2Config(vocab_size=320, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=16, num_key_value_heads=1, head_dim=128, max_position_embeddings=8192,
+                      rope_theta=10000.0)
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(seed)
+    m = Qwen2ForCausalLM(cfg).eval()
+    with torch.no_grad():  # sharper attention than the default 0.02 init
+        for layer in m.model.layers:
+            layer.self_attn.q_proj.weight.mul_(6.0)
+            layer.self_attn.k_proj.weight.mul_(6.0)
+    return m.to(device=device, dtype=dtype)
+
+
+def surgery_copy(model, device=None, dtype=None):
+    from dvattention_amd import hf
+    m = copy.deepcopy(model)
+    if device is not None:
+        m = m.to(device=device, dtype=dtype)
+    hf.model_surgery(m)
+    return m
+
+
+def ref_logits(model, tokens):
+    """transformers' own forward (eager attention, no cache) on one sequence."""
+    with torch.no_grad():
+        return model(input_ids=tokens[None]).logits[0].float()
+
+
+def run_steps(model, cache, steps):
+    """Feed ``steps`` = list of [W, S] token tensors; returns the logits of each."""
+    outs = []
+    with torch.no_grad():
+        for ids in steps:
+            out = model(**cache.get_input_kwargs(ids))
+            outs.append(out.logits.float())
+    return outs
+
+
+def single_worker(model, ops, dtype, device, P=11, steps=3, seed=1):
+    from dvattention_amd import hf
+    g = torch.Generator().manual_seed(seed)
+    toks = torch.randint(0, 320, (P + steps,), generator=g).to(device)
+    pool = hf.SegmentPool(model.config, 1, 64, dtype, device)
+    cache = hf.DVAttnCache([[pool[0]]], model, ops=ops)
+    feeds = [toks[:P][None]] + [toks[P + i:P + i + 1][None] for i in range(steps - 1)]
+    return toks, run_steps(model, cache, feeds)
+
+
+def independent_workers(model, ops, dtype, device, P=9, steps=3, seed=2):
+    """A shared prompt segment, then two workers that each see [prompt, own]."""
+    from dvattention_amd import hf
+    g = torch.Generator().manual_seed(seed)
+    prompt = torch.randint(0, 320, (P,), generator=g).to(device)
+    own = torch.randint(0, 320, (2, steps), generator=g).to(device)
+    pool = hf.SegmentPool(model.config, 3, 64, dtype, device)
+    pre = hf.DVAttnCache([[pool[0]]], model, ops=ops)
+    run_steps(model, pre, [prompt[None]])
+    cache = hf.DVAttnCache([[pool[0], pool[1]], [pool[0], pool[2]]], model, ops=ops)
+    outs = run_steps(model, cache, [own[:, i:i + 1] for i in range(steps)])
+    return prompt, own, outs
+
+
+# ------------------------------------------------------------------ CPU --
+
+def test_single_worker_matches_transformers_cpu():
+    model = tiny_qwen2(torch.float32, "cpu")
+    ours = surgery_copy(model)
+    toks, outs = single_worker(ours, OracleOps, torch.float32, "cpu")
+    P = 11
+    ref = ref_logits(model, toks[:P + 2])
+    assert torch.allclose(outs[0][0], ref[:P], atol=1e-4, rtol=1e-4)
+    for i, o in enumerate(outs[1:]):
+        assert torch.allclose(o[0, -1], ref[P + i], atol=1e-4, rtol=1e-4)
+
+
+def test_independent_workers_match_transformers_cpu():
+    model = tiny_qwen2(torch.float32, "cpu")
+    ours = surgery_copy(model)
+    prompt, own, outs = independent_workers(ours, OracleOps, torch.float32, "cpu")
+    for w in range(2):
+        ref = ref_logits(model, torch.cat([prompt, own[w]]))
+        for i, o in enumerate(outs):
+            assert torch.allclose(o[w, -1], ref[len(prompt) + i], atol=1e-4, rtol=1e-4), (w, i)
+
+
+def test_cache_positions_and_views_cpu():
+    """Left padding: masked tokens are not written and do not advance the
+    worker's segment; locations follow each worker's own segment order."""
+    from dvattention_amd import hf
+    model = surgery_copy(tiny_qwen2(torch.float32, "cpu"))
+    pool = hf.SegmentPool(model.config, 3, 32, torch.float32, "cpu")
+    cache = hf.DVAttnCache([[pool[0], pool[2], pool[1]], [pool[0], pool[1], pool[2]]], model, ops=OracleOps)
+    ids = torch.tensor([[5, 6, 7], [8, 9, 10]])
+    mask = torch.tensor([[0, 1, 1], [1, 1, 1]])
+    with torch.no_grad():
+        model(**cache.get_input_kwargs(ids, mask))
+    assert [pool[1].get_seq_length(l) for l in range(2)] == [2, 2]
+    assert [pool[2].get_seq_length(l) for l in range(2)] == [3, 3]
+    assert pool[0].get_seq_length() == 0
+    # views ordered as worker 0's structure: [seg0, seg2, seg1]; worker 0 sees 0,2,1 and
+    # worker 1 sees 0,1,2 (suffix sums of lengths 0 / 3 / 2, minus S=3, plus s)
+    want = torch.tensor([[[2, 3, 4], [2, 3, 4]], [[2, 3, 4], [0, 1, 2]], [[-1, 0, 1], [2, 3, 4]]], dtype=torch.int32)
+    assert torch.equal(cache.locations, want)
+    assert torch.all(pool.k[0][1, :, 2:] == 0)  # nothing past the two real tokens
+
+
+# ------------------------------------------------------------------ GPU --
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 5e-4), (torch.bfloat16, 6e-2)])
+def test_single_worker_matches_transformers_gpu(gpu, dtype, tol):
+    from dvattention_amd import hf
+    model = tiny_qwen2(dtype, gpu)
+    ours = surgery_copy(model)
+    toks, outs = single_worker(ours, hf.HipOps, dtype, gpu)
+    P = 11
+    ref = ref_logits(model, toks[:P + 2])
+    err = (outs[0][0] - ref[:P]).abs().max().item()
+    for i, o in enumerate(outs[1:]):
+        err = max(err, (o[0, -1] - ref[P + i]).abs().max().item())
+    assert err <= tol, err
+
+
+@pytest.mark.gpu
+def test_independent_workers_match_transformers_gpu(gpu):
+    from dvattention_amd import hf
+    model = tiny_qwen2(torch.bfloat16, gpu)
+    ours = surgery_copy(model)
+    prompt, own, outs = independent_workers(ours, hf.HipOps, torch.bfloat16, gpu)
+    for w in range(2):
+        ref = ref_logits(model, torch.cat([prompt, own[w]]))
+        for i, o in enumerate(outs):
+            err = (o[w, -1] - ref[len(prompt) + i]).abs().max().item()
+            assert err <= 6e-2, (w, i, err)
+
+
+@pytest.mark.gpu
+def test_cross_visible_workers_and_merge_match_oracle_gpu(gpu):
+    """Two workers that see each other's segments ([prompt, other, own]), then
+    merge_caches of worker 1 into worker 0: the HIP run against the same module
+    code on the CPU oracle, fp32."""
+    from dvattention_amd import hf
+    base = tiny_qwen2(torch.float32, "cpu", seed=3)
+    m_gpu = surgery_copy(base, gpu, torch.float32)
+    m_cpu = surgery_copy(base)
+    g = torch.Generator().manual_seed(4)
+    prompt = torch.randint(0, 320, (7,), generator=g)
+    own = torch.randint(0, 320, (2, 4), generator=g)
+    results = []
+    for model, ops, dev in ((m_gpu, hf.HipOps, gpu), (m_cpu, OracleOps, "cpu")):
+        pool = hf.SegmentPool(model.config, 3, 64, torch.float32, dev)
+        run_steps(model, hf.DVAttnCache([[pool[0]]], model, ops=ops), [prompt[None].to(dev)])
+        cache = hf.DVAttnCache([[pool[0], pool[2], pool[1]], [pool[0], pool[1], pool[2]]], model, ops=ops)
+        outs = run_steps(model, cache, [own[:, i:i + 1].to(dev) for i in range(3)])
+        hf.merge_caches(pool[1], pool[2], model, ops=ops)
+        solo = hf.DVAttnCache([[pool[0], pool[1]]], model, ops=ops)
+        outs += run_steps(model, solo, [own[:1, 3:4].to(dev)])
+        results.append(([o.cpu() for o in outs], [pool.k[0].cpu(), pool.v[1].cpu()]))
+    (a, ca), (b, cb) = results
+    for x, y in zip(a, b):
+        assert torch.allclose(x, y, atol=5e-4, rtol=1e-4), (x - y).abs().max().item()
+    for x, y in zip(ca, cb):
+        assert torch.allclose(x, y, atol=1e-5, rtol=1e-5)
