@@ -613,9 +613,152 @@ __device__ inline void compute(SoftState& st, const unsigned char* kt, const uns
     mfma_settle(st.o);
 }
 
+constexpr int kStreamViews = 4;  // views of one piece streamed back to back
+
+// The visible keys [v0, v1) of up to four paged views of one row (vm: their
+// lanes in the view table t) streamed back to back: the views' page ids (one
+// shared page cache) and rotated queries are loaded first, then one stage loop
+// runs over the concatenated key ranges, so a view boundary does not drain the
+// two-stage ring.  Returns false, having done nothing, when the views' pages
+// do not fit the page cache.
+template <int DT, int QM, int RM>
+__device__ bool views_stream(const DecodeParams& p, unsigned char* wlds, int row, int w, int hkv, long long v0,
+                             long long v1, uint64_t vm, const ViewTab& t, SoftState& st) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t ring = __builtin_amdgcn_readfirstlane(lds_addr(wlds));
+    int* pc = reinterpret_cast<int*>(wlds + kRing * kStage);
+    int vf[kStreamViews], l0[kStreamViews], l1[kStreamViews], ns[kStreamViews], pcb[kStreamViews + 1];
+    int voff[kStreamViews], lpa[kStreamViews];
+    int npages = 0, N = 0;
+    uint64_t m = vm;
+#pragma unroll
+    for (int j = 0; j < kStreamViews; ++j) {
+        const bool has = m != 0;
+        const int f = has ? __builtin_ctzll(m) : 0;
+        m &= m - 1;
+        const int vis = __shfl(t.vis, f, kWave);
+        const long long P = __shfl(t.P, f, kWave);
+        const long long off = __shfl(t.off, f, kWave);
+        const long long a = v0 > P ? v0 : P;
+        const long long b = v1 < P + vis ? v1 : P + vis;
+        vf[j] = f;
+        l0[j] = has ? (int)(a - P) : 0;
+        l1[j] = has ? (int)(b - P) : 0;
+        ns[j] = (l1[j] - l0[j] + kStep - 1) / kStep;
+        N += ns[j];
+        voff[j] = (int)off;
+        lpa[j] = 0;
+        pcb[j] = npages;
+        if (has) {
+            uint32_t la, lz, r;
+            const int pa = voff[j] + l0[j], pz = voff[j] + l1[j] - 1;
+            page_split(p, pa > 0 ? (uint32_t)pa : 0u, la, r);
+            page_split(p, pz > 0 ? (uint32_t)pz : 0u, lz, r);
+            lpa[j] = (int)la;
+            npages += (int)(lz - la) + 1;
+        }
+    }
+    pcb[kStreamViews] = npages;
+    if (npages > kPc) return false;
+    const int* bt = p.bt + (long long)w * p.maxB;
+#pragma unroll
+    for (int j = 0; j < kStreamViews; ++j) {
+        const int need = pcb[j + 1] - pcb[j];
+        for (int i = lane; i < need; i += kWave) {
+            const uint32_t lp = (uint32_t)lpa[j] + (uint32_t)i;
+            int pg = lp < (uint32_t)p.maxB ? bt[lp] : -1;
+            if (pg < 0 || pg >= p.nblocks) pg = -1;
+            pc[pcb[j] + i] = pg;
+        }
+    }
+
+    // issue cursor: view ji, next key li; the view's parameters are copied out of
+    // the per-view arrays with constant indices (no dynamically indexed arrays,
+    // which would live in scratch memory)
+    View vi;
+    vi.hkv = hkv;
+    vi.k = reinterpret_cast<const unsigned char*>(p.kc);
+    vi.v = reinterpret_cast<const unsigned char*>(p.vc);
+    vi.off = voff[0];
+    vi.lp0 = lpa[0];
+    vi.b = l1[0];
+    const int* pci = pc;
+    int ji = 0, li = l0[0];
+    auto advance = [&]() {
+        li += kStep;
+        if (li >= vi.b) {
+            ++ji;
+#pragma unroll
+            for (int k = 1; k < kStreamViews; ++k)
+                if (k == ji) {
+                    vi.off = voff[k];
+                    vi.lp0 = lpa[k];
+                    vi.b = l1[k];
+                    pci = pc + pcb[k];
+                    li = l0[k];
+                }
+        }
+    };
+    uint32_t m0 = issue<kKvPaged>(p, vi, pci, ring, li);
+    advance();
+    uint32_t m1 = 0;
+    if (N > 1) {
+        m1 = issue<kKvPaged>(p, vi, pci, ring + kStage, li);
+        advance();
+    }
+    // rotated queries of every view while the first stages are in flight, then
+    // settled (a query load pending at the loop would make the compiler wait
+    // for all vector memory in every step)
+    u32x4 q[kStreamViews][4];
+#pragma unroll
+    for (int j = 0; j < kStreamViews; ++j) {
+        if (ns[j] > 0) {
+            load_q16<DT, QM, RM>(p, row, vf[j], hkv, q[j]);
+        } else {
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) q[j][cc] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kStreamViews; ++j)
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) asm volatile("" : "+v"(q[j][cc]));
+    u32x4 qc[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) qc[cc] = q[0][cc];
+    int jc = 0, left = ns[0];
+    for (int s = 0; s < N; ++s) {
+        if (s + 1 < N) wait_vmcnt<16>();
+        else wait_vmcnt<0>();
+        const unsigned char* kt = wlds + (s & 1) * kStage;
+        compute<DT>(st, kt, kt + kTile, (s & 1) ? m1 : m0, qc, p.l2scale);
+        if (s + 2 < N) {
+            lds_wait();  // the slot's reads are complete before it is refilled
+            const uint32_t mk = issue<kKvPaged>(p, vi, pci, ring + (uint32_t)((s & 1) * kStage), li);
+            advance();
+            if (s & 1) m1 = mk;
+            else m0 = mk;
+        }
+        if (--left == 0 && s + 1 < N) {
+            ++jc;
+#pragma unroll
+            for (int k = 1; k < kStreamViews; ++k)
+                if (k == jc) {
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) qc[cc] = q[k][cc];
+                    left = ns[k];
+                }
+        }
+    }
+    lds_wait();
+    return true;
+}
+
 // One wave: KV head hkv over visible keys [v0, v1) of one row.  wlds: this
-// wave's LDS (ring, then page cache).
-template <int DT, int QM, int KVM, int RM>
+// wave's LDS (ring, then page cache).  MV: paged rows of several views stream
+// them back to back (a separate instantiation, so single-view launches keep
+// their own register allocation).
+template <int DT, int QM, int KVM, int RM, bool MV>
 __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int hkv, long long v0, long long v1,
                       bool final_out, int slot, int wv) {
     const int lane = threadIdx.x & 63;
@@ -635,7 +778,7 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
 
     // P: visible keys of the earlier views; off: logical position of view f
     // (paged): sum of the earlier fragment_lengths
-    for_views<KVM, RM>(p, row, v0, v1, [&](int f, int vis, long long P, long long off) {
+    auto one_view = [&](int f, int vis, long long P, long long off) {
         const long long a = v0 > P ? v0 : P;
         const long long bnd = v1 < P + vis ? v1 : P + vis;
         {
@@ -706,7 +849,23 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
                 sa = sb;
             }
         }
-    });
+    };
+    if (p.F <= kWave) {
+        const ViewTab t = view_table<KVM, RM>(p, row);
+        uint64_t vm = ballot(lane < p.F && t.vis > 0 && t.P < v1 && t.P + t.vis > v0);
+        const int nv = __builtin_popcountll(vm);
+        bool done = false;
+        if constexpr (MV && KVM == kKvPaged) {
+            if (nv >= 2 && nv <= kStreamViews) done = views_stream<DT, QM, RM>(p, wlds, row, w, hkv, v0, v1, vm, t, st);
+        }
+        while (!done && vm) {
+            const int f = __builtin_ctzll(vm);
+            vm &= vm - 1;
+            one_view(f, __shfl(t.vis, f, kWave), __shfl(t.P, f, kWave), __shfl(t.off, f, kWave));
+        }
+    } else {
+        for_views<KVM, RM>(p, row, v0, v1, one_view);
+    }
 
     // epilogue: total over the four lane groups, normalise, base-2 LSE
     const float lt = rows4_sum(st.l);
@@ -738,7 +897,7 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
 
 }  // namespace stream
 
-template <int DT, int QM, int KVM, int RM>
+template <int DT, int QM, int KVM, int RM, bool MV>
 __global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
     extern __shared__ __align__(16) unsigned char smem[];
     __shared__ long long s_scan[4];
@@ -748,7 +907,7 @@ __global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
     unsigned char* wlds = smem + wv * stream::kWaveLds;
     run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<KVM, RM>(p, row); },
                  [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
-        if (wv < HPW) stream::piece<DT, QM, KVM, RM>(p, wlds, row, hg * HPW + wv, v0, v1, fin, slot, wv);
+        if (wv < HPW) stream::piece<DT, QM, KVM, RM, MV>(p, wlds, row, hg * HPW + wv, v0, v1, fin, slot, wv);
     });
 }
 
@@ -875,10 +1034,10 @@ int wgs_per_cu(int hpw) { return 8 / hpw; }
 
 // The decode kernel for a dtype: the LDS-streaming kernel for 16-bit types,
 // the register-staged one for fp32.
-template <int DT, int QM, int KVM, int RM>
+template <int DT, int QM, int KVM, int RM, bool MV>
 const void* decode_kernel() {
     if constexpr (DT == kF32) return reinterpret_cast<const void*>(&dv_decode<DT, QM, KVM, RM>);
-    else return reinterpret_cast<const void*>(&dv_stream<DT, QM, KVM, RM>);
+    else return reinterpret_cast<const void*>(&dv_stream<DT, QM, KVM, RM, MV>);
 }
 
 template <int DT>
@@ -888,7 +1047,7 @@ size_t wave_lds() {
 
 // Resident workgroups per CU for one kernel instance at a given dynamic LDS
 // size, cached per 1 KiB of LDS (hipOccupancy queries cost host time).
-template <int DT, int QM, int KVM, int RM>
+template <int DT, int QM, int KVM, int RM, bool MV>
 int resident_wgs(int hpw, size_t lds) {
     static int cache[4][161];  // [hpw-1][lds KiB]; 0 = not queried yet
     const int kib = (int)((lds + 1023) / 1024);
@@ -896,7 +1055,7 @@ int resident_wgs(int hpw, size_t lds) {
     int& slot = cache[hpw - 1][kib];
     if (slot == 0) {
         int nb = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_kernel<DT, QM, KVM, RM>(), hpw * kWave,
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_kernel<DT, QM, KVM, RM, MV>(), hpw * kWave,
                                                          (size_t)kib * 1024) != hipSuccess ||
             nb < 1)
             nb = 1;
@@ -905,10 +1064,10 @@ int resident_wgs(int hpw, size_t lds) {
     return slot;
 }
 
-template <int DT, int QM, int KVM, int RM>
+template <int DT, int QM, int KVM, int RM, bool MV>
 hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, hipStream_t stream) {
     const size_t lds = (size_t)p.hpw * wave_lds<DT>() + (size_t)(p.nrows + 1) * sizeof(long long);
-    const void* kern = decode_kernel<DT, QM, KVM, RM>();
+    const void* kern = decode_kernel<DT, QM, KVM, RM, MV>();
     static bool attr_set = false;
     if (!attr_set) {
         // largest dynamic LDS any launch of this kernel asks for (4 waves, kMaxRows rows)
@@ -918,14 +1077,14 @@ hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, 
         attr_set = true;
     }
     // one wave of workgroups that are all resident at once, bounded by the work
-    long long nwg = (long long)cus * resident_wgs<DT, QM, KVM, RM>(p.hpw, lds);
+    long long nwg = (long long)cus * resident_wgs<DT, QM, KVM, RM, MV>(p.hpw, lds);
     if (nwg > max_wg) nwg = max_wg;
     if (nwg > cap) nwg = cap;
     p.nwg = nwg < 1 ? 1 : (int)nwg;
     if constexpr (DT == kF32)
         hipLaunchKernelGGL((dv_decode<DT, QM, KVM, RM>), dim3(p.nwg), dim3(p.hpw * kWave), lds, stream, p);
     else
-        hipLaunchKernelGGL((dv_stream<DT, QM, KVM, RM>), dim3(p.nwg), dim3(p.hpw * kWave), lds, stream, p);
+        hipLaunchKernelGGL((dv_stream<DT, QM, KVM, RM, MV>), dim3(p.nwg), dim3(p.hpw * kWave), lds, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return note_site(e, "launch decode");
     const int nseg = p.nrows * (p.Hkv / p.hpw);
@@ -939,11 +1098,14 @@ template <int DT>
 hipError_t dispatch_modes(int qmode, int kvmode, int rowmode, const DecodeParams& p, long long max_wg,
                           long long cap, int cus, hipStream_t stream) {
     if (kvmode == kKvPaged && qmode == kQRotFull && rowmode == kRowWS)
-        return launch_one<DT, kQRotFull, kKvPaged, kRowWS>(p, max_wg, cap, cus, stream);
+        return p.F >= 2 && DT != kF32 ? launch_one<DT, kQRotFull, kKvPaged, kRowWS, true>(p, max_wg, cap, cus, stream)
+                                       : launch_one<DT, kQRotFull, kKvPaged, kRowWS, false>(p, max_wg, cap, cus, stream);
     if (kvmode == kKvPaged && qmode == kQRotHalf && rowmode == kRowVarlen)
-        return launch_one<DT, kQRotHalf, kKvPaged, kRowVarlen>(p, max_wg, cap, cus, stream);
+        return p.F >= 2 && DT != kF32
+                   ? launch_one<DT, kQRotHalf, kKvPaged, kRowVarlen, true>(p, max_wg, cap, cus, stream)
+                   : launch_one<DT, kQRotHalf, kKvPaged, kRowVarlen, false>(p, max_wg, cap, cus, stream);
     if (kvmode == kKvContig && qmode == kQPre && rowmode == kRowWS)
-        return launch_one<DT, kQPre, kKvContig, kRowWS>(p, max_wg, cap, cus, stream);
+        return launch_one<DT, kQPre, kKvContig, kRowWS, false>(p, max_wg, cap, cus, stream);
     return hipErrorInvalidValue;
 }
 
