@@ -70,6 +70,7 @@ struct DecodeParams {
     int nwg;              // workgroups launched
     int min_keys;         // smallest key range worth a workgroup
     int piece_cost;       // fixed cost of starting a segment, in keys (charged in the work split)
+    int skew_pm;          // per mille of a chunk moved from each odd workgroup to the even one before it
     int slot_floats;      // floats per partial slot
     FragDesc frags[kMaxFragArgs];
 };

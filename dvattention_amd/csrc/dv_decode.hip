@@ -23,6 +23,8 @@
 //    otherwise the pieces go to fp32 partial slots (normalised output + base-2
 //    log-sum-exp) and dv_merge combines them, as the reference's reduce kernels
 //    do (paged_kernel_v21.cuh:307-374).
+#include <stdlib.h>
+
 #include "dv_common.h"
 #include "dv_device.h"
 #include "dv_schedule.h"
@@ -1029,6 +1031,19 @@ int pick_hpw(int Hkv) {
 // time a workgroup needs to restart its pipeline on a new segment.
 constexpr int kPieceCost = 128;
 
+// Per mille of a chunk the work split moves from each odd workgroup (odd XCD)
+// to the even one before it: measured on MI355X, the odd XCD of each pair ends
+// 5-8 % later with equal chunks, and 40-60 per mille gave the shortest calls
+// on configurations 2-4.  DVATTN_XCD_SKEW_PM overrides it (0: equal chunks).
+int xcd_skew_pm() {
+    static const int v = [] {
+        const char* e = getenv("DVATTN_XCD_SKEW_PM");
+        const int x = e ? atoi(e) : 50;
+        return x < 0 ? 0 : (x > 200 ? 200 : x);
+    }();
+    return v;
+}
+
 // workgroups per CU such that about eight waves share a CU
 int wgs_per_cu(int hpw) { return 8 / hpw; }
 
@@ -1150,6 +1165,7 @@ hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const De
     p.part = reinterpret_cast<float*>(workspace);
     p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
     p.piece_cost = dtype == kF32 ? 0 : kPieceCost;
+    p.skew_pm = xcd_skew_pm();
     for (int r0 = 0; r0 < nrows_total; r0 += kMaxRows) {
         p.row_begin = r0;
         p.nrows = nrows_total - r0 < kMaxRows ? nrows_total - r0 : kMaxRows;

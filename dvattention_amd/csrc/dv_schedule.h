@@ -63,12 +63,26 @@ __device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s
     if (tid == 0) s_pref[nrows] = total;
     __syncthreads();
 
-    // 2. equal chunks of the cost space; segment (r, hg) spans D_r cost units at
-    //    NHG*pref[r] + hg*D_r, its keys the last D_r - c of them
+    // 2. chunks of the cost space; segment (r, hg) spans D_r cost units at
+    //    NHG*pref[r] + hg*D_r, its keys the last D_r - c of them.  Workgroups are
+    //    dispatched to the XCDs round robin (workgroup i on XCD i % 8) and the odd
+    //    XCD of each pair streams a few percent slower, so chunk 2k is `skew` cost
+    //    units longer and chunk 2k+1 as much shorter than the mean (p.skew_pm per
+    //    mille; 0: equal chunks).  Chunk i spans [bound(i), bound(i + 1)).
     const long long Wc = total * NHG;
     const long long ng = (Wc + p.min_keys - 1) / p.min_keys;
     const int geff = Wc == 0 ? 0 : (int)(ng < p.nwg ? ng : p.nwg);
     const long long chunk = geff ? (Wc + geff - 1) / geff : 1;
+    const long long skew = chunk * p.skew_pm / 1000;
+    auto bound = [&](long long i) {
+        const long long b = i * chunk + ((i & 1) ? skew : 0);
+        return b < Wc ? b : Wc;
+    };
+    // chunk holding cost position x (< Wc)
+    auto chunk_of = [&](long long x) {
+        const long long k = x / (2 * chunk);
+        return 2 * k + (x - 2 * k * chunk >= chunk + skew ? 1 : 0);
+    };
 
     if (blockIdx.x == 0) {
         for (int sg = tid; sg < nrows * NHG; sg += nthreads) {
@@ -77,7 +91,7 @@ __device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s
             int base = 0, cnt = 0;
             if (D > 0) {
                 const long long segc = NHG * s_pref[r] + hg * D;
-                const long long gf = (segc + c) / chunk, gl = (segc + D - 1) / chunk;
+                const long long gf = chunk_of(segc + c), gl = chunk_of(segc + D - 1);
                 cnt = (int)(gl - gf + 1);
                 base = (int)gf + sg;
             }
@@ -88,8 +102,8 @@ __device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s
     const int gidx = blockIdx.x;
     if (gidx >= geff) return;
 
-    long long u = gidx * chunk;
-    const long long uend = u + chunk < Wc ? u + chunk : Wc;
+    long long u = bound(gidx);
+    const long long uend = bound(gidx + 1);
     // last row r with NHG*pref[r] <= u
     int lo = 0, hi = nrows - 1;
     while (lo < hi) {
@@ -112,7 +126,7 @@ __device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s
         const long long b = uend < segc + D ? uend : segc + D;
         if (a < b) {
             const int sg = r * NHG + hg;
-            const long long gf = ka / chunk, gl = (segc + D - 1) / chunk;
+            const long long gf = chunk_of(ka), gl = chunk_of(segc + D - 1);
             const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
             piece(p.row_begin + r, hg, a - ka, b - ka, gl == gf, slot);
         }
