@@ -451,7 +451,7 @@ __global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
     const int NHG = p.Hkv;  // one KV head per workgroup
 
     run_schedule(p, NHG, s_pref, s_scan, [&](int rg) { return group_visible<KVM>(p, rg); },
-                 [&](int rg, int hg, long long v0, long long v1, bool fin, int slot) {
+                 [&](int rg, int hg, long long v0, long long v1, bool fin, int slot, long long) {
                      chunk_piece<DT, QM, KVM>(p, smem, pages, rg, hg, v0, v1, fin, slot);
                  });
 }

@@ -486,7 +486,7 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
     long long* s_pref = reinterpret_cast<long long*>(smem + HPW * vt_bytes<DT>());
     unsigned char* vt = smem + wv * vt_bytes<DT>();
     run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<KVM, RM>(p, row); },
-                 [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
+                 [&](int row, int hg, long long v0, long long v1, bool fin, int slot, long long rk) {
         if (wv < HPW) process_piece<DT, QM, KVM, RM>(p, vt, row, hg * HPW + wv, v0, v1, fin, slot, wv);
     });
 }
@@ -762,15 +762,32 @@ __device__ bool views_stream(const DecodeParams& p, unsigned char* wlds, int row
 // their own register allocation).
 template <int DT, int QM, int KVM, int RM, bool MV>
 __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int hkv, long long v0, long long v1,
-                      bool final_out, int slot, int wv) {
+                      bool final_out, int slot, int wv, long long row_keys) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, n = lane & 15;
     const uint32_t ring = __builtin_amdgcn_readfirstlane(lds_addr(wlds));
     int* pc = reinterpret_cast<int*>(wlds + kRing * kStage);
 
+    // the row's sequence (varlen: the first 64 sequence bounds) and its view
+    // table are loaded in one round trip; one view needs no loads: its visible
+    // keys are the row's, counted by the schedule
+    int cu = 0x7fffffff;
+    if (RM == kRowVarlen) cu = lane < p.W ? p.cu_q[lane + 1] : 0x7fffffff;
+    ViewTab t;
+    if (p.F == 1) {
+        t.vis = lane == 0 ? (int)row_keys : 0;
+        t.P = 0;
+        t.off = 0;
+    } else if (p.F <= kWave) {
+        t = view_table<KVM, RM>(p, row);
+    }
     int w;
-    if (RM == kRowVarlen) w = varlen_seq(p, row);
-    else w = row / p.S;
+    if (RM == kRowVarlen) {
+        const uint64_t b = ballot(lane < p.W && row < cu);
+        w = b ? __builtin_ctzll(b) : varlen_seq(p, row);
+    } else {
+        w = row / p.S;
+    }
 
     SoftState st;
 #pragma unroll
@@ -853,7 +870,6 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
         }
     };
     if (p.F <= kWave) {
-        const ViewTab t = view_table<KVM, RM>(p, row);
         uint64_t vm = ballot(lane < p.F && t.vis > 0 && t.P < v1 && t.P + t.vis > v0);
         const int nv = __builtin_popcountll(vm);
         bool done = false;
@@ -908,8 +924,8 @@ __global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
     long long* s_pref = reinterpret_cast<long long*>(smem + HPW * stream::kWaveLds);
     unsigned char* wlds = smem + wv * stream::kWaveLds;
     run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<KVM, RM>(p, row); },
-                 [&](int row, int hg, long long v0, long long v1, bool fin, int slot) {
-        if (wv < HPW) stream::piece<DT, QM, KVM, RM, MV>(p, wlds, row, hg * HPW + wv, v0, v1, fin, slot, wv);
+                 [&](int row, int hg, long long v0, long long v1, bool fin, int slot, long long rk) {
+        if (wv < HPW) stream::piece<DT, QM, KVM, RM, MV>(p, wlds, row, hg * HPW + wv, v0, v1, fin, slot, wv, rk);
     });
 }
 

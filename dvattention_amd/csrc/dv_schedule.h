@@ -15,11 +15,19 @@ namespace dv {
 // new segment thus gets fewer real keys.  Per-row cost prefix sums live in LDS
 // (s_pref, nrows + 1 entries; s_scan: one entry per wave).  Workgroup 0 writes
 // the merge directory (segment -> first partial slot, piece count).  Then
-// piece(row, head_group, v0, v1, final, slot) runs for each piece of this
-// workgroup's chunk: visible keys [v0, v1) of the segment, `final` when the
-// segment has no other piece, `slot` its partial slot.  Slots are
+// piece(row, head_group, v0, v1, final, slot, row_keys) runs for each piece of
+// this workgroup's chunk: visible keys [v0, v1) of the segment, `final` when
+// the segment has no other piece, `slot` its partial slot, `row_keys` the row's
+// visible key count.  Slots are
 // sg + workgroup index, increasing along the cost space, so they are unique and
 // below nwg + nrows * NHG.
+// a / b for non-negative operands, in 32 bits when both fit (a 64-bit division
+// is a long instruction sequence on the GPU)
+__device__ inline long long udiv(long long a, long long b) {
+    if (((unsigned long long)(a | b) >> 32) == 0) return (long long)((uint32_t)a / (uint32_t)b);
+    return a / b;
+}
+
 template <class RowKeys, class PieceFn>
 __device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s_pref, long long* s_scan,
                                     RowKeys&& row_keys, PieceFn&& piece) {
@@ -70,17 +78,17 @@ __device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s
     //    units longer and chunk 2k+1 as much shorter than the mean (p.skew_pm per
     //    mille; 0: equal chunks).  Chunk i spans [bound(i), bound(i + 1)).
     const long long Wc = total * NHG;
-    const long long ng = (Wc + p.min_keys - 1) / p.min_keys;
+    const long long ng = udiv(Wc + p.min_keys - 1, p.min_keys);
     const int geff = Wc == 0 ? 0 : (int)(ng < p.nwg ? ng : p.nwg);
-    const long long chunk = geff ? (Wc + geff - 1) / geff : 1;
-    const long long skew = chunk * p.skew_pm / 1000;
+    const long long chunk = geff ? udiv(Wc + geff - 1, geff) : 1;
+    const long long skew = udiv(chunk * p.skew_pm, 1000);
     auto bound = [&](long long i) {
         const long long b = i * chunk + ((i & 1) ? skew : 0);
         return b < Wc ? b : Wc;
     };
     // chunk holding cost position x (< Wc)
     auto chunk_of = [&](long long x) {
-        const long long k = x / (2 * chunk);
+        const long long k = udiv(x, 2 * chunk);
         return 2 * k + (x - 2 * k * chunk >= chunk + skew ? 1 : 0);
     };
 
@@ -119,7 +127,7 @@ __device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s
             ++r;
             continue;
         }
-        const int hg = (int)((u - rs) / D);
+        const int hg = (int)udiv(u - rs, D);
         const long long segc = rs + hg * D;  // the segment's cost range [segc, segc + D)
         const long long ka = segc + c;       // its keys: cost positions [ka, segc + D)
         const long long a = u > ka ? u : ka;
@@ -128,7 +136,7 @@ __device__ inline void run_schedule(const DecodeParams& p, int NHG, long long* s
             const int sg = r * NHG + hg;
             const long long gf = chunk_of(ka), gl = chunk_of(segc + D - 1);
             const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
-            piece(p.row_begin + r, hg, a - ka, b - ka, gl == gf, slot);
+            piece(p.row_begin + r, hg, a - ka, b - ka, gl == gf, slot, D - c);
         }
         u = segc + D;
     }
