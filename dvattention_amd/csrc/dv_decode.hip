@@ -383,7 +383,7 @@ __device__ inline void load_q32(const DecodeParams& p, int row, int f, int hkv, 
 
 template <int DT, int QM, int KVM, int RM>
 __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row, int hkv, long long v0,
-                              long long v1, bool final_out, int slot, int wv) {
+                              long long v1, bool final_out, int slot, int wv, long long row_keys) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, n = lane & 15;
 
@@ -403,7 +403,7 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
 
     // P: visible keys of the earlier views; off: logical position of view f
     // (paged): sum of the earlier fragment_lengths
-    for_views<KVM, RM>(p, row, v0, v1, [&](int f, int vis, long long P, long long off) {
+    auto one_view = [&](int f, int vis, long long P, long long off) {
         const long long a = v0 > P ? v0 : P;
         const long long bnd = v1 < P + vis ? v1 : P + vis;
         {
@@ -427,15 +427,26 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
             }
             static_assert(DT == kF32, "16-bit types use dv_stream");
             f32x4 qB[8];
+            // the first stage's K/V loads go out before the query's, so the two
+            // round trips overlap
+            Kv32 b;
+            window_update<DT, KVM>(p, c, win, l0, l1);
+            issue32<KVM>(p, c, win, b, l0, l1);
             load_q32<QM, RM>(p, row, f, hkv, qB);
-            for (int l = l0; l < l1; l += kStep) {
-                Kv32 b;
+            compute32(st, b, qB, vt, p.l2scale);
+            for (int l = l0 + kStep; l < l1; l += kStep) {
                 window_update<DT, KVM>(p, c, win, l, l1);
                 issue32<KVM>(p, c, win, b, l, l1);
                 compute32(st, b, qB, vt, p.l2scale);
             }
         }
-    });
+    };
+    if (p.F == 1) {
+        // one view: its visible keys are the row's, counted by the schedule
+        if (row_keys > 0 && v1 > v0) one_view(0, (int)row_keys, 0ll, 0ll);
+    } else {
+        for_views<KVM, RM>(p, row, v0, v1, one_view);
+    }
 
     // epilogue: total over the four lane groups, normalise, base-2 LSE
     const float lt = rows4_sum(st.l);
@@ -487,7 +498,7 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
     unsigned char* vt = smem + wv * vt_bytes<DT>();
     run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<KVM, RM>(p, row); },
                  [&](int row, int hg, long long v0, long long v1, bool fin, int slot, long long rk) {
-        if (wv < HPW) process_piece<DT, QM, KVM, RM>(p, vt, row, hg * HPW + wv, v0, v1, fin, slot, wv);
+        if (wv < HPW) process_piece<DT, QM, KVM, RM>(p, vt, row, hg * HPW + wv, v0, v1, fin, slot, wv, rk);
     });
 }
 
@@ -1181,6 +1192,9 @@ hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const De
     p.part = reinterpret_cast<float*>(workspace);
     p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
     p.piece_cost = dtype == kF32 ? 0 : kPieceCost;
+    // the fp32 kernel waits for each 32-key stage before the next: one stage per
+    // workgroup is worth it on small problems
+    if (dtype == kF32 && p.min_keys > kStep) p.min_keys = kStep;
     p.skew_pm = xcd_skew_pm();
     for (int r0 = 0; r0 < nrows_total; r0 += kMaxRows) {
         p.row_begin = r0;
