@@ -587,6 +587,10 @@ hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& ba
     p.part = reinterpret_cast<float*>(workspace);
     p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
     p.piece_cost = chunk::kPieceCost;
+    // odd workgroups (odd XCD of each pair) take shorter chunks, as in the decode
+    // split; 30 per mille measured best on configuration 5
+    static const int skew = env_per_mille("DVATTN_CHUNK_SKEW_PM", 30);
+    p.skew_pm = skew;
     for (long long g0 = 0; g0 < groups_total; g0 += kMaxRows) {
         p.row_begin = (int)g0;
         p.nrows = (int)(groups_total - g0 < kMaxRows ? groups_total - g0 : kMaxRows);

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 namespace dv {
 
@@ -114,6 +115,13 @@ struct MetaParams {
     int round_dt;             // -1, or a 16-bit dtype code the values are rounded through
     int F, W, S, R;
 };
+
+// A per-mille tuning value from the environment, clamped to [0, 200].
+inline int env_per_mille(const char* name, int dflt) {
+    const char* e = getenv(name);
+    const int x = e ? atoi(e) : dflt;
+    return x < 0 ? 0 : (x > 200 ? 200 : x);
+}
 
 // Internal launchers (return a hipError_t; argument validation happens in the C ABI).
 size_t decode_workspace_bytes(int nrows_total, int Hkv, int device, int dtype);

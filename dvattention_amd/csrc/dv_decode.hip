@@ -1063,11 +1063,7 @@ constexpr int kPieceCost = 128;
 // 5-8 % later with equal chunks, and 40-60 per mille gave the shortest calls
 // on configurations 2-4.  DVATTN_XCD_SKEW_PM overrides it (0: equal chunks).
 int xcd_skew_pm() {
-    static const int v = [] {
-        const char* e = getenv("DVATTN_XCD_SKEW_PM");
-        const int x = e ? atoi(e) : 50;
-        return x < 0 ? 0 : (x > 200 ? 200 : x);
-    }();
+    static const int v = env_per_mille("DVATTN_XCD_SKEW_PM", 50);
     return v;
 }
 
