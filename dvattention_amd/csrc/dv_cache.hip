@@ -126,8 +126,10 @@ __global__ __launch_bounds__(256) void dv_kv_append(const AppendParams p, uint32
     }
     if (page < 0 || page >= p.nblocks) return;
     const long long row = ps - (long long)lp * p.bs;
-    if (has_k) store_run<raw, RUN>(reinterpret_cast<raw*>(p.kc) + page * p.kcs[0] + row * p.kcs[1] + h * p.kcs[2] + d0, xa);
-    if (has_v) store_run<raw, RUN>(reinterpret_cast<raw*>(p.vc) + page * p.vcs[0] + row * p.vcs[1] + h * p.vcs[2] + d0, vo);
+    if (has_k)
+        store_run<raw, RUN>(reinterpret_cast<raw*>(p.kc) + page * p.kcs[0] + row * p.kcs[1] + h * p.kcs[2] + d0, xa);
+    if (has_v)
+        store_run<raw, RUN>(reinterpret_cast<raw*>(p.vc) + page * p.vcs[0] + row * p.vcs[1] + h * p.vcs[2] + d0, vo);
 }
 
 template <int DT, int CDT, int RUN>

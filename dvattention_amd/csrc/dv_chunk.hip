@@ -526,14 +526,13 @@ size_t lds_bytes(int nrows) {
 }
 
 template <int DT, int QM, int KVM>
-hipError_t launch(DecodeParams p, int cus, long long cap, hipStream_t stream) {
-    static bool attr = false;
-    if (!attr) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_chunk<DT, QM, KVM>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes(kMaxRows));
-        if (e != hipSuccess) return e;
-        attr = true;
-    }
+hipError_t launch(DecodeParams p, int device, int cus, long long cap, hipStream_t stream) {
+    static std::atomic<unsigned long long> attr_done{0};
+    hipError_t ea = once_per_device(attr_done, device, [] {
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_chunk<DT, QM, KVM>),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes(kMaxRows));
+    });
+    if (ea != hipSuccess) return ea;
     const size_t lds = lds_bytes(p.nrows);
     long long nwg = cus;  // one eight-wave workgroup per CU (LDS ring 96 KiB)
     if (nwg > cap) nwg = cap;
@@ -548,11 +547,7 @@ hipError_t launch(DecodeParams p, int cus, long long cap, hipStream_t stream) {
 }  // namespace chunk
 
 namespace {
-int chunk_cus(int device) {
-    int c = 0;
-    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c <= 0) c = 256;
-    return c;
-}
+int chunk_cus(int device) { return device_cu_count(device); }
 }  // namespace
 
 size_t chunk_workspace_bytes(int W, int S, int Hkv, int device) {
@@ -596,13 +591,13 @@ hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& ba
         p.nrows = (int)(groups_total - g0 < kMaxRows ? groups_total - g0 : kMaxRows);
         const long long cap = ((long long)p.nrows * p.Hkv * max_keys_per_group + p.min_keys - 1) / p.min_keys;
         if (dtype == kBF16 && qmode == kQRotFull && kvmode == kKvPaged)
-            e = chunk::launch<kBF16, kQRotFull, kKvPaged>(p, cus, cap, stream);
+            e = chunk::launch<kBF16, kQRotFull, kKvPaged>(p, device, cus, cap, stream);
         else if (dtype == kF16 && qmode == kQRotFull && kvmode == kKvPaged)
-            e = chunk::launch<kF16, kQRotFull, kKvPaged>(p, cus, cap, stream);
+            e = chunk::launch<kF16, kQRotFull, kKvPaged>(p, device, cus, cap, stream);
         else if (dtype == kBF16 && qmode == kQPre && kvmode == kKvContig)
-            e = chunk::launch<kBF16, kQPre, kKvContig>(p, cus, cap, stream);
+            e = chunk::launch<kBF16, kQPre, kKvContig>(p, device, cus, cap, stream);
         else if (dtype == kF16 && qmode == kQPre && kvmode == kKvContig)
-            e = chunk::launch<kF16, kQPre, kKvContig>(p, cus, cap, stream);
+            e = chunk::launch<kF16, kQPre, kKvContig>(p, device, cus, cap, stream);
         else
             e = hipErrorInvalidValue;
         if (e != hipSuccess) return e;

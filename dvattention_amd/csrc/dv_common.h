@@ -5,6 +5,8 @@
 
 #include <hip/hip_runtime.h>
 #include <stddef.h>
+
+#include <atomic>
 #include <stdint.h>
 #include <stdlib.h>
 
@@ -115,6 +117,30 @@ struct MetaParams {
     int round_dt;             // -1, or a 16-bit dtype code the values are rounded through
     int F, W, S, R;
 };
+
+// CU count of a device, queried once per device (thread-safe; 256 if unknown).
+inline int device_cu_count(int device) {
+    static std::atomic<int> cache[64];
+    if (device < 0 || device >= 64) return 256;
+    int c = cache[device].load(std::memory_order_relaxed);
+    if (c == 0) {
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c <= 0) c = 256;
+        cache[device].store(c, std::memory_order_relaxed);
+    }
+    return c;
+}
+
+// Runs set_up() the first time a kernel is launched on `device` (one bit per
+// device in `done`).  set_up must be idempotent: two threads launching at once
+// may both run it.
+template <class F>
+inline hipError_t once_per_device(std::atomic<unsigned long long>& done, int device, F&& set_up) {
+    const unsigned long long bit = device >= 0 && device < 64 ? 1ull << device : 0ull;
+    if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+    const hipError_t e = set_up();
+    if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
+    return e;
+}
 
 // A per-mille tuning value from the environment, clamped to [0, 200].
 inline int env_per_mille(const char* name, int dflt) {

@@ -1029,24 +1029,7 @@ hipError_t note_site(hipError_t e, const char* site) {
     return e;
 }
 
-struct DevInfo {
-    int cus = 0;
-    bool init = false;
-};
-
-DevInfo g_dev[64];
-
-int device_cus(int device) {
-    if (device < 0 || device >= 64) return 256;
-    DevInfo& d = g_dev[device];
-    if (!d.init) {
-        int c = 0;
-        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || c <= 0) c = 256;
-        d.cus = c;
-        d.init = true;
-    }
-    return d.cus;
-}
+int device_cus(int device) { return device_cu_count(device); }
 
 int pick_hpw(int Hkv) {
     if (Hkv % 4 == 0) return 4;
@@ -1087,33 +1070,32 @@ size_t wave_lds() {
 // size, cached per 1 KiB of LDS (hipOccupancy queries cost host time).
 template <int DT, int QM, int KVM, int RM, bool MV>
 int resident_wgs(int hpw, size_t lds) {
-    static int cache[4][161];  // [hpw-1][lds KiB]; 0 = not queried yet
+    static std::atomic<int> cache[4][161];  // [hpw-1][lds KiB]; 0 = not queried yet
     const int kib = (int)((lds + 1023) / 1024);
     if (kib > 160 || hpw < 1 || hpw > 4) return 1;
-    int& slot = cache[hpw - 1][kib];
-    if (slot == 0) {
-        int nb = 0;
+    std::atomic<int>& slot = cache[hpw - 1][kib];
+    int nb = slot.load(std::memory_order_relaxed);
+    if (nb == 0) {
         if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, decode_kernel<DT, QM, KVM, RM, MV>(), hpw * kWave,
                                                          (size_t)kib * 1024) != hipSuccess ||
             nb < 1)
             nb = 1;
-        slot = nb;
+        slot.store(nb, std::memory_order_relaxed);
     }
-    return slot;
+    return nb;
 }
 
 template <int DT, int QM, int KVM, int RM, bool MV>
-hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, hipStream_t stream) {
+hipError_t launch_one(DecodeParams p, int device, long long max_wg, long long cap, int cus, hipStream_t stream) {
     const size_t lds = (size_t)p.hpw * wave_lds<DT>() + (size_t)(p.nrows + 1) * sizeof(long long);
     const void* kern = decode_kernel<DT, QM, KVM, RM, MV>();
-    static bool attr_set = false;
-    if (!attr_set) {
+    static std::atomic<unsigned long long> attr_done{0};
+    const hipError_t ea = once_per_device(attr_done, device, [&] {
         // largest dynamic LDS any launch of this kernel asks for (4 waves, kMaxRows rows)
         const size_t max_lds = (size_t)kMaxWavesPerWg * wave_lds<DT>() + (size_t)(kMaxRows + 1) * sizeof(long long);
-        hipError_t e = hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
-        if (e != hipSuccess) return note_site(e, "hipFuncSetAttribute(decode)");
-        attr_set = true;
-    }
+        return hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
+    });
+    if (ea != hipSuccess) return note_site(ea, "hipFuncSetAttribute(decode)");
     // one wave of workgroups that are all resident at once, bounded by the work
     long long nwg = (long long)cus * resident_wgs<DT, QM, KVM, RM, MV>(p.hpw, lds);
     if (nwg > max_wg) nwg = max_wg;
@@ -1133,17 +1115,18 @@ hipError_t launch_one(DecodeParams p, long long max_wg, long long cap, int cus, 
 }
 
 template <int DT>
-hipError_t dispatch_modes(int qmode, int kvmode, int rowmode, const DecodeParams& p, long long max_wg,
+hipError_t dispatch_modes(int qmode, int kvmode, int rowmode, const DecodeParams& p, int device, long long max_wg,
                           long long cap, int cus, hipStream_t stream) {
     if (kvmode == kKvPaged && qmode == kQRotFull && rowmode == kRowWS)
-        return p.F >= 2 && DT != kF32 ? launch_one<DT, kQRotFull, kKvPaged, kRowWS, true>(p, max_wg, cap, cus, stream)
-                                       : launch_one<DT, kQRotFull, kKvPaged, kRowWS, false>(p, max_wg, cap, cus, stream);
+        return p.F >= 2 && DT != kF32
+                   ? launch_one<DT, kQRotFull, kKvPaged, kRowWS, true>(p, device, max_wg, cap, cus, stream)
+                   : launch_one<DT, kQRotFull, kKvPaged, kRowWS, false>(p, device, max_wg, cap, cus, stream);
     if (kvmode == kKvPaged && qmode == kQRotHalf && rowmode == kRowVarlen)
         return p.F >= 2 && DT != kF32
-                   ? launch_one<DT, kQRotHalf, kKvPaged, kRowVarlen, true>(p, max_wg, cap, cus, stream)
-                   : launch_one<DT, kQRotHalf, kKvPaged, kRowVarlen, false>(p, max_wg, cap, cus, stream);
+                   ? launch_one<DT, kQRotHalf, kKvPaged, kRowVarlen, true>(p, device, max_wg, cap, cus, stream)
+                   : launch_one<DT, kQRotHalf, kKvPaged, kRowVarlen, false>(p, device, max_wg, cap, cus, stream);
     if (kvmode == kKvContig && qmode == kQPre && rowmode == kRowWS)
-        return launch_one<DT, kQPre, kKvContig, kRowWS, false>(p, max_wg, cap, cus, stream);
+        return launch_one<DT, kQPre, kKvContig, kRowWS, false>(p, device, max_wg, cap, cus, stream);
     return hipErrorInvalidValue;
 }
 
@@ -1198,9 +1181,9 @@ hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const De
         // enough workgroups to fill the chip, never more than the key count allows
         const long long cap = ((long long)p.nrows * nhg * max_keys_per_row + p.min_keys - 1) / p.min_keys;
         switch (dtype) {
-            case kBF16: e = dispatch_modes<kBF16>(qmode, kvmode, rowmode, p, max_wg, cap, cus, stream); break;
-            case kF16: e = dispatch_modes<kF16>(qmode, kvmode, rowmode, p, max_wg, cap, cus, stream); break;
-            case kF32: e = dispatch_modes<kF32>(qmode, kvmode, rowmode, p, max_wg, cap, cus, stream); break;
+            case kBF16: e = dispatch_modes<kBF16>(qmode, kvmode, rowmode, p, device, max_wg, cap, cus, stream); break;
+            case kF16: e = dispatch_modes<kF16>(qmode, kvmode, rowmode, p, device, max_wg, cap, cus, stream); break;
+            case kF32: e = dispatch_modes<kF32>(qmode, kvmode, rowmode, p, device, max_wg, cap, cus, stream); break;
             default: e = hipErrorInvalidValue;
         }
         if (e != hipSuccess) return e;

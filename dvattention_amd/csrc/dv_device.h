@@ -196,7 +196,8 @@ __device__ inline void softmax32(f32x4 (&o)[8], float& m, float& l, const f32x4&
     if (mask == 0xffffffffu && l2scale > 0.0f) {
         // every key visible, positive scale: max of the raw scores, scaled once,
         // and p = exp2(s * l2scale - m) in one fma
-        float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])), fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
+        float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                         fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
         const float nm = -update(rows4_max(mx) * l2scale);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
