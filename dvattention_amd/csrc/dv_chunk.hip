@@ -37,6 +37,7 @@ constexpr int kKvBytes = kStep * 256;         // one K (or V) stage tile: 32 key
 constexpr int kStageBytes = 2 * kKvBytes;     // K tile then V tile
 constexpr int kRingBytes = kStages * kStageBytes;
 constexpr int kPageCap = 2048;                // page ids cached in LDS per view sub-range
+constexpr int kVPre = 8;                      // V^T slices read ahead of the softmax (of 8)
 constexpr int kDmaPerStage = 2;               // per wave: 1 x K + 1 x V (1 KiB = 4 key rows each)
 
 // Start cost of a piece in the work split, in keys (query staging and rotation,
@@ -44,6 +45,15 @@ constexpr int kDmaPerStage = 2;               // per wave: 1 x K + 1 x V (1 KiB 
 constexpr int kPieceCost = 256;
 
 static __device__ __align__(16) unsigned char zrow[512];
+
+// threadIdx.x behind an empty asm statement: per-lane addresses derived from it
+// are recomputed where they are used instead of being hoisted out of the view
+// loop and held in registers across the stage loop.
+__device__ inline int opaque_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
 
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
@@ -113,12 +123,77 @@ struct Tile {
     float m, l;
 };
 
-// Online softmax of one tile for one 32-key stage (softmax32); returns the P^T
-// MFMA operand.
+// Online softmax of one tile for one 32-key stage; returns the P^T MFMA operand.
+// Same arithmetic as softmax32 (dv_device.h): p = exp2(s * l2scale - m), with
+// the running max m raised (and the accumulators rescaled) only when a row's
+// scaled score exceeds it by more than kMaxSlack.  The common case -- every key
+// visible and no score over the slack -- needs no row reduction: a wave in
+// which any lane holds a score over the slack (or a row with no key yet,
+// m = -inf) takes the exact path, which raises the max.
 template <int DT>
 __device__ inline u32x4 tile_softmax(Tile& t, const f32x4& s0, const f32x4& s1, uint32_t mask, float l2scale) {
     float pr[8];
-    softmax32(t.o, t.m, t.l, s0, s1, mask, l2scale, pr);
+    const bool full = mask == 0xffffffffu && l2scale > 0.0f;
+    bool exact = true;  // wave-uniform
+    float mx;           // the row's scaled max, on the exact path
+    if (full) {
+        const float nm = -t.m;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pr[i] = __builtin_fmaf(s0[i], l2scale, nm);
+            pr[4 + i] = __builtin_fmaf(s1[i], l2scale, nm);
+        }
+        const float lmx =
+            fmaxf(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])), fmaxf(fmaxf(pr[4], pr[5]), fmaxf(pr[6], pr[7])));
+        exact = ballot(lmx > kMaxSlack) != 0;
+        // max of the raw scores, scaled once
+        if (exact)
+            mx = rows4_max(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                 fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])))) *
+                 l2scale;
+    } else {
+        // bit g*4 + i (+16) of the mask: the per-lane shift sits behind an empty
+        // asm so the eight bit masks are not precomputed and held in registers
+        // across the stage loop
+        uint32_t mg = mask >> (((opaque_tid() & 63) >> 4) * 4);
+        asm volatile("" : "+v"(mg));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pr[i] = ((mg >> i) & 1u) ? s0[i] * l2scale : -DV_INF;
+            pr[4 + i] = ((mg >> (16 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
+        }
+        mx = rows4_max(
+            fmaxf(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])), fmaxf(fmaxf(pr[4], pr[5]), fmaxf(pr[6], pr[7]))));
+    }
+    if (exact) {
+        // raise the running max where some row exceeds it by more than the slack
+        // (one site rescales the accumulators)
+        if (ballot(mx > t.m + kMaxSlack)) {
+            const float mnew = fmaxf(t.m, mx);
+            const float alpha = mnew == -DV_INF ? 1.0f : __builtin_amdgcn_exp2f(t.m - mnew);
+            t.l *= alpha;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) t.o[c] *= alpha;
+            t.m = mnew;
+        }
+        const float m = t.m == -DV_INF ? 0.0f : t.m;  // p = 0 while the row has no visible key
+        if (full) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                pr[i] = __builtin_fmaf(s0[i], l2scale, -m);
+                pr[4 + i] = __builtin_fmaf(s1[i], l2scale, -m);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pr[i] -= m;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(pr[i]);
+    float ps = pr[0];
+#pragma unroll
+    for (int i = 1; i < 8; ++i) ps += pr[i];
+    t.l += ps;
     return u32x4{pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]), pack2<DT>(pr[6], pr[7])};
 }
 
@@ -133,7 +208,7 @@ __device__ inline void stage_q_tiles(const DecodeParams& p, unsigned char* qreg,
                                      int ntile, int f, int hkv, u32x4 (&qB)[kTiles][4]) {
 #pragma clang fp contract(off)
     using raw = typename Tr<DT>::raw;
-    const int lane = threadIdx.x & 63;
+    const int lane = opaque_tid() & 63;
     const int g = lane >> 4, n = lane & 15;
     const uint32_t qbase = lds_addr(qreg);
     for (int t = 0; t < ntile; ++t) {
@@ -277,7 +352,8 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
             vis_blk = v > vis_blk ? v : vis_blk;
         }
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) vis_t[t] = t < ntile ? view_vis<KVM>(p, f, loc_of(p, f, w, tok0 + t)) : 0;
+        for (int t = 0; t < kTiles; ++t)  // wave-uniform: the stage masks and their branches stay scalar
+            vis_t[t] = __builtin_amdgcn_readfirstlane(t < ntile ? view_vis<KVM>(p, f, loc_of(p, f, w, tok0 + t)) : 0);
         const long long a = v0 > P ? v0 : P;
         const long long bnd = v1 < P + vis_blk ? v1 : P + vis_blk;
         if (a < bnd) {
@@ -361,18 +437,45 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                         s1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
                     }
                     // K row n (and 16 + n), piece (cc*4 + g) ^ n: the swizzle only flips
-                    // address bits 6-7 of kbase, so slice cc is at kbase ^ (64 cc)
+                    // address bits 6-7 of kbase, so slice cc is at kbase ^ (64 cc).  All
+                    // eight operand reads are issued before the first MFMA, so their LDS
+                    // latency overlaps the MFMAs instead of preceding each pair.
                     const uint32_t kbase = lds_addr(kt) + (uint32_t)(n * 256 + 16 * (g ^ (n & 3)) + 64 * (n >> 2));
+                    u32x4 ka[4], kb[4];
 #pragma unroll
                     for (int cc = 0; cc < 4; ++cc) {
-                        const u32x4 a0 = lds_read16_at(kbase ^ (uint32_t)(64 * cc));
-                        const u32x4 a1 = lds_read16_at((kbase ^ (uint32_t)(64 * cc)) + 16 * 256);
+                        ka[cc] = lds_read16_at(kbase ^ (uint32_t)(64 * cc));
+                        kb[cc] = lds_read16_at((kbase ^ (uint32_t)(64 * cc)) + 16 * 256);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int cc = 0; cc < 4; ++cc) {
 #pragma unroll
                         for (int t = 0; t < kTiles; ++t) {
-                            s0[t] = Tr<DT>::mma(a0, qB[t][cc], s0[t]);
-                            s1[t] = Tr<DT>::mma(a1, qB[t][cc], s1[t]);
+                            s0[t] = Tr<DT>::mma(ka[cc], qB[t][cc], s0[t]);
+                            s1[t] = Tr<DT>::mma(kb[cc], qB[t][cc], s1[t]);
                         }
                     }
+                    // V^T operands (the first kVPre slices read before the softmax, so
+                    // their latency overlaps it; the rest before the P V MFMAs, behind
+                    // the first slices' MFMAs): block lane sl -> key g*4 + sl/4 (+16),
+                    // dims cc*16 + (sl%4)*4;
+                    // row k0 (and k0 + 16), piece (cc*2 + b) ^ ((k0 & 7) << 1), byte hb:
+                    // the swizzle only flips address bits 5-7 of vbase, so slice cc is
+                    // at vbase ^ (32 cc)
+                    const int sl = lane & 15;
+                    const int k0 = g * 4 + (sl >> 2);
+                    const uint32_t vbase = lds_addr(vt) + (uint32_t)(k0 * 256 + 16 * ((sl & 3) >> 1) + (sl & 1) * 8 +
+                                                                     32 * (k0 & 7));
+                    u32x4 va[8];
+                    auto read_v = [&](int cc) {
+                        const u32x2 a0 = lds_read_tr16_at(vbase ^ (uint32_t)(32 * cc));
+                        const u32x2 a1 = lds_read_tr16_at((vbase ^ (uint32_t)(32 * cc)) + 16 * 256);
+                        va[cc] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+                    };
+#pragma unroll
+                    for (int cc = 0; cc < kVPre; ++cc) read_v(cc);
+                    __builtin_amdgcn_sched_barrier(0);
                     u32x4 pB[kTiles];
 #pragma unroll
                     for (int t = 0; t < kTiles; ++t) {
@@ -380,25 +483,14 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                         const uint32_t lm = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
                         pB[t] = tile_softmax<DT>(tl[t], s0[t], s1[t], okmask & lm, p.l2scale);
                     }
-                    // O^T += V^T P^T: block lane sl -> key g*4 + sl/4 (+16), dims
-                    // cc*16 + (sl%4)*4; each 16-dim slice of V^T is read once for both tiles
-                    {
-                        // row k0 (and k0 + 16), piece (cc*2 + b) ^ ((k0 & 7) << 1), byte hb:
-                        // the swizzle only flips address bits 5-7 of vbase, so slice cc is
-                        // at vbase ^ (32 cc)
-                        const int sl = lane & 15;
-                        const int k0 = g * 4 + (sl >> 2);
-                        const uint32_t vbase = lds_addr(vt) + (uint32_t)(k0 * 256 + 16 * ((sl & 3) >> 1) +
-                                                                         (sl & 1) * 8 + 32 * (k0 & 7));
+                    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                        for (int cc = 0; cc < 8; ++cc) {
-                            const u32x2 a0 = lds_read_tr16_at(vbase ^ (uint32_t)(32 * cc));
-                            const u32x2 a1 = lds_read_tr16_at((vbase ^ (uint32_t)(32 * cc)) + 16 * 256);
-                            const u32x4 va = {a0[0], a0[1], a1[0], a1[1]};
+                    for (int cc = kVPre; cc < 8; ++cc) read_v(cc);
+                    // O^T += V^T P^T; each 16-dim slice of V^T serves both tiles
 #pragma unroll
-                            for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va, pB[t], tl[t].o[cc]);
-                        }
-                    }
+                    for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+                        for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va[cc], pB[t], tl[t].o[cc]);
 #pragma unroll
                     for (int t = 0; t < kTiles; ++t) mfma_settle(tl[t].o);
                     lds_barrier();  // every wave is done with this stage before it is refilled
@@ -412,6 +504,9 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
     }
 
     // epilogue: per tile, normalise and write the output or a partial slot
+    {
+    const int lane = opaque_tid() & 63;
+    const int g = lane >> 4, n = lane & 15;
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) {
         if (t >= ntile) continue;
@@ -436,6 +531,7 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
             for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(o + c * 16 + g * 4) = tl[t].o[c] * inv;
             if (g == 0) sbase[kTokBlk * kGqa * kHeadDim + tb * kGqa + n] = lt > 0.0f ? tl[t].m + log2f(lt) : -DV_INF;
         }
+    }
     }
 }
 

@@ -216,8 +216,9 @@ __device__ inline void softmax32(f32x4 (&o)[8], float& m, float& l, const f32x4&
 #pragma unroll
         for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - mm);
     }
+    ps = pr[0];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) ps += pr[i];
+    for (int i = 1; i < 8; ++i) ps += pr[i];
     l += ps;
 }
 
