@@ -46,15 +46,6 @@ constexpr int kPieceCost = 256;
 
 static __device__ __align__(16) unsigned char zrow[512];
 
-// threadIdx.x behind an empty asm statement: per-lane addresses derived from it
-// are recomputed where they are used instead of being hoisted out of the view
-// loop and held in registers across the stage loop.
-__device__ inline int opaque_tid() {
-    int t = threadIdx.x;
-    asm volatile("" : "+v"(t));
-    return t;
-}
-
 __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // swizzled 16-byte piece positions inside a 256-byte key row
@@ -123,77 +114,12 @@ struct Tile {
     float m, l;
 };
 
-// Online softmax of one tile for one 32-key stage; returns the P^T MFMA operand.
-// Same arithmetic as softmax32 (dv_device.h): p = exp2(s * l2scale - m), with
-// the running max m raised (and the accumulators rescaled) only when a row's
-// scaled score exceeds it by more than kMaxSlack.  The common case -- every key
-// visible and no score over the slack -- needs no row reduction: a wave in
-// which any lane holds a score over the slack (or a row with no key yet,
-// m = -inf) takes the exact path, which raises the max.
+// Online softmax of one tile for one 32-key stage (softmax32); returns the P^T
+// MFMA operand.
 template <int DT>
 __device__ inline u32x4 tile_softmax(Tile& t, const f32x4& s0, const f32x4& s1, uint32_t mask, float l2scale) {
     float pr[8];
-    const bool full = mask == 0xffffffffu && l2scale > 0.0f;
-    bool exact = true;  // wave-uniform
-    float mx;           // the row's scaled max, on the exact path
-    if (full) {
-        const float nm = -t.m;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pr[i] = __builtin_fmaf(s0[i], l2scale, nm);
-            pr[4 + i] = __builtin_fmaf(s1[i], l2scale, nm);
-        }
-        const float lmx =
-            fmaxf(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])), fmaxf(fmaxf(pr[4], pr[5]), fmaxf(pr[6], pr[7])));
-        exact = ballot(lmx > kMaxSlack) != 0;
-        // max of the raw scores, scaled once
-        if (exact)
-            mx = rows4_max(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
-                                 fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])))) *
-                 l2scale;
-    } else {
-        // bit g*4 + i (+16) of the mask: the per-lane shift sits behind an empty
-        // asm so the eight bit masks are not precomputed and held in registers
-        // across the stage loop
-        uint32_t mg = mask >> (((opaque_tid() & 63) >> 4) * 4);
-        asm volatile("" : "+v"(mg));
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pr[i] = ((mg >> i) & 1u) ? s0[i] * l2scale : -DV_INF;
-            pr[4 + i] = ((mg >> (16 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
-        }
-        mx = rows4_max(
-            fmaxf(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])), fmaxf(fmaxf(pr[4], pr[5]), fmaxf(pr[6], pr[7]))));
-    }
-    if (exact) {
-        // raise the running max where some row exceeds it by more than the slack
-        // (one site rescales the accumulators)
-        if (ballot(mx > t.m + kMaxSlack)) {
-            const float mnew = fmaxf(t.m, mx);
-            const float alpha = mnew == -DV_INF ? 1.0f : __builtin_amdgcn_exp2f(t.m - mnew);
-            t.l *= alpha;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) t.o[c] *= alpha;
-            t.m = mnew;
-        }
-        const float m = t.m == -DV_INF ? 0.0f : t.m;  // p = 0 while the row has no visible key
-        if (full) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                pr[i] = __builtin_fmaf(s0[i], l2scale, -m);
-                pr[4 + i] = __builtin_fmaf(s1[i], l2scale, -m);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) pr[i] -= m;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(pr[i]);
-    float ps = pr[0];
-#pragma unroll
-    for (int i = 1; i < 8; ++i) ps += pr[i];
-    t.l += ps;
+    softmax32(t.o, t.m, t.l, s0, s1, mask, l2scale, pr);
     return u32x4{pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]), pack2<DT>(pr[6], pr[7])};
 }
 

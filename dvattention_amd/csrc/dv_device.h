@@ -113,6 +113,15 @@ __device__ inline u32x4 lds_read16_at(uint32_t addr) {
 
 __device__ inline void compiler_fence() { asm volatile("" ::: "memory"); }
 
+// threadIdx.x behind an empty asm statement: per-lane values derived from it are
+// recomputed where they are used instead of being hoisted out of loops and held
+// in registers across them.
+__device__ inline int opaque_tid() {
+    int t = threadIdx.x;
+    asm volatile("" : "+v"(t));
+    return t;
+}
+
 // ---- direct-to-LDS loads ------------------------------------------------------
 
 __device__ inline uint32_t lds_addr(const void* p) {
@@ -176,12 +185,47 @@ constexpr float kMaxSlack = 8.0f;
 // (p = exp2(score * l2scale - m)).  Updates the running max m, sum l and the
 // accumulators o (rescaled when m is raised); returns the unnormalised p of the
 // lane's 8 keys (keys g*4 + i, then 16 + g*4 + i).
+//
+// The common case -- every key visible and no score over the slack -- needs no
+// row reduction: a wave in which any lane holds a score over the slack (or a
+// row with no key yet, m = -inf) takes the exact path, which raises the max to
+// the rows' maximum.  The accumulators are rescaled at one site, so the register
+// allocator keeps them in place across the paths.
 __device__ inline void softmax32(f32x4 (&o)[8], float& m, float& l, const f32x4& s0, const f32x4& s1,
                                  uint32_t mask, float l2scale, float (&pr)[8]) {
-    const int g = (threadIdx.x & 63) >> 4;
-    // raise the running max (rescaling the accumulators) if some row needs it;
-    // returns the max to subtract (0 while the row has no visible key: p = 0)
-    auto update = [&](float mx) -> float {
+    const bool full = mask == 0xffffffffu && l2scale > 0.0f;
+    bool exact = true;  // wave-uniform
+    float mx;           // the row's scaled max, on the exact path
+    if (full) {
+        const float nm = -m;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pr[i] = __builtin_fmaf(s0[i], l2scale, nm);
+            pr[4 + i] = __builtin_fmaf(s1[i], l2scale, nm);
+        }
+        const float lmx =
+            fmaxf(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])), fmaxf(fmaxf(pr[4], pr[5]), fmaxf(pr[6], pr[7])));
+        exact = ballot(lmx > kMaxSlack) != 0;
+        // max of the raw scores, scaled once
+        if (exact)
+            mx = rows4_max(fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
+                                 fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])))) *
+                 l2scale;
+    } else {
+        // bit g*4 + i (+16) of the mask: the per-lane shift sits behind an empty
+        // asm so the eight bit masks are not precomputed and held in registers
+        uint32_t mg = mask >> (((opaque_tid() & 63) >> 4) * 4);
+        asm volatile("" : "+v"(mg));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            pr[i] = ((mg >> i) & 1u) ? s0[i] * l2scale : -DV_INF;
+            pr[4 + i] = ((mg >> (16 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
+        }
+        mx = rows4_max(
+            fmaxf(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])), fmaxf(fmaxf(pr[4], pr[5]), fmaxf(pr[6], pr[7]))));
+    }
+    if (exact) {
+        // raise the running max where some row exceeds it by more than the slack
         if (ballot(mx > m + kMaxSlack)) {
             const float mnew = fmaxf(m, mx);
             const float alpha = mnew == -DV_INF ? 1.0f : __builtin_amdgcn_exp2f(m - mnew);
@@ -190,33 +234,21 @@ __device__ inline void softmax32(f32x4 (&o)[8], float& m, float& l, const f32x4&
             for (int c = 0; c < 8; ++c) o[c] *= alpha;
             m = mnew;
         }
-        return m == -DV_INF ? 0.0f : m;
-    };
-    float ps = 0.0f;
-    if (mask == 0xffffffffu && l2scale > 0.0f) {
-        // every key visible, positive scale: max of the raw scores, scaled once,
-        // and p = exp2(s * l2scale - m) in one fma
-        float mx = fmaxf(fmaxf(fmaxf(s0[0], s0[1]), fmaxf(s0[2], s0[3])),
-                         fmaxf(fmaxf(s1[0], s1[1]), fmaxf(s1[2], s1[3])));
-        const float nm = -update(rows4_max(mx) * l2scale);
+        const float mm = m == -DV_INF ? 0.0f : m;  // p = 0 while the row has no visible key
+        if (full) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s0[i], l2scale, nm));
-            pr[4 + i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s1[i], l2scale, nm));
+            for (int i = 0; i < 4; ++i) {
+                pr[i] = __builtin_fmaf(s0[i], l2scale, -mm);
+                pr[4 + i] = __builtin_fmaf(s1[i], l2scale, -mm);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) pr[i] -= mm;
         }
-    } else {
-        float x[8];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            x[i] = ((mask >> (g * 4 + i)) & 1u) ? s0[i] * l2scale : -DV_INF;
-            x[4 + i] = ((mask >> (16 + g * 4 + i)) & 1u) ? s1[i] * l2scale : -DV_INF;
-        }
-        float mx = fmaxf(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])), fmaxf(fmaxf(x[4], x[5]), fmaxf(x[6], x[7])));
-        const float mm = update(rows4_max(mx));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(x[i] - mm);
     }
-    ps = pr[0];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(pr[i]);
+    float ps = pr[0];
 #pragma unroll
     for (int i = 1; i < 8; ++i) ps += pr[i];
     l += ps;
