@@ -37,7 +37,7 @@ constexpr int kKvBytes = kStep * 256;         // one K (or V) stage tile: 32 key
 constexpr int kStageBytes = 2 * kKvBytes;     // K tile then V tile
 constexpr int kRingBytes = kStages * kStageBytes;
 constexpr int kPageCap = 2048;                // page ids cached in LDS per view sub-range
-constexpr int kVPre = 8;                      // V^T slices read ahead of the softmax (of 8)
+constexpr int kAhead = 4;                     // stages in flight ahead of the one computed
 constexpr int kDmaPerStage = 2;               // per wave: 1 x K + 1 x V (1 KiB = 4 key rows each)
 
 // Start cost of a piece in the work split, in keys (query staging and rotation,
@@ -46,7 +46,13 @@ constexpr int kPieceCost = 256;
 
 static __device__ __align__(16) unsigned char zrow[512];
 
-__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Workgroup barrier that is also a compiler memory and scheduling barrier: no
+// LDS access or MFMA moves across it.
+__device__ inline void wg_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
+    asm volatile("s_barrier" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+}
 
 // swizzled 16-byte piece positions inside a 256-byte key row
 __device__ inline int swz_k(int key, int piece) { return piece ^ (key & 15); }
@@ -246,6 +252,34 @@ __device__ inline long long group_visible(const DecodeParams& p, int rg) {
     return best;
 }
 
+// O^T += V^T P^T of one stage for both tiles: block lane sl -> key g*4 + sl/4
+// (+16), dims cc*16 + (sl%4)*4; row k0 (and k0 + 16), piece (cc*2 + b) ^
+// ((k0 & 7) << 1), byte hb: the swizzle only flips address bits 5-7 of vbase, so
+// slice cc is at vbase ^ (32 cc).  Each 16-dim slice of V^T is read once for both
+// tiles; all sixteen reads are issued before the first MFMA.
+template <int DT>
+__device__ inline void pv_stage(const unsigned char* vt, const u32x4 (&pB)[kTiles], Tile (&tl)[kTiles]) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, sl = lane & 15;
+    const int k0 = g * 4 + (sl >> 2);
+    const uint32_t vbase =
+        lds_addr(vt) + (uint32_t)(k0 * 256 + 16 * ((sl & 3) >> 1) + (sl & 1) * 8 + 32 * (k0 & 7));
+    u32x4 va[8];
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) {
+        const u32x2 a0 = lds_read_tr16_at(vbase ^ (uint32_t)(32 * cc));
+        const u32x2 a1 = lds_read_tr16_at((vbase ^ (uint32_t)(32 * cc)) + 16 * 256);
+        va[cc] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+        for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va[cc], pB[t], tl[t].o[cc]);
+#pragma unroll
+    for (int t = 0; t < kTiles; ++t) mfma_settle(tl[t].o);
+}
+
 // One workgroup: keys [v0, v1) of row group rg for KV head hkv.
 template <int DT, int QM, int KVM>
 __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pages, int rg, int hkv, long long v0,
@@ -333,26 +367,29 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                     r.pages_ok = __syncthreads_and(ok) != 0;
                 }
                 const int nsteps = (sbnd - sa + kStep - 1) / kStep;
-                // prologue: stages 0 .. kStages-2 (past the end: rows of zeros)
+                // Ping-pong: the stage loop alternates an MFMA cluster X_i (S = K Q^T of
+                // stage i, O += V P of stage i - 1) and a VALU cluster Y_i (softmax of
+                // stage i, then the loads of stage i + kAhead), with a workgroup barrier
+                // between clusters.  Waves 4-7 start one cluster behind waves 0-3 (wave
+                // w runs on SIMD w % 4), so the two waves of each SIMD run X and Y at
+                // the same time.  Every wave passes 2 * nsteps + 1 barriers.  Ring slot
+                // (i + kAhead) % kStages held stage i - 2, whose V was last read in
+                // X_{i-1}, finished by both groups before either starts Y_i.
+                // uniform in the wave (a scalar branch: the group's extra barrier must
+                // not execute with an empty exec mask in the other group's waves)
+                const int grp = __builtin_amdgcn_readfirstlane(wv >> 2);
+                const unsigned char* vt_prev = smem;  // V tile of the previous stage
+                u32x4 pB[kTiles] = {};                 // its P^T operands
+                // prologue: stages 0 .. kAhead-1 (past the end: rows of zeros)
 #pragma unroll
-                for (int st = 0; st < kStages - 1; ++st) issue_stage<KVM>(p, r, pages, ring, st, sa + st * kStep);
+                for (int st = 0; st < kAhead; ++st) issue_stage<KVM>(p, r, pages, ring, st, sa + st * kStep);
+                wait_vmcnt<kDmaPerStage * (kAhead - 1)>();  // own share of stage 0 landed
+                if (grp) wg_barrier();
                 for (int i = 0; i < nsteps; ++i) {
-                    issue_stage<KVM>(p, r, pages, ring, i + kStages - 1, sa + (i + kStages - 1) * kStep);
-                    wait_vmcnt<kDmaPerStage * (kStages - 1)>();
-                    __builtin_amdgcn_s_barrier();
+                    wg_barrier();  // stage i landed for every wave
+                    // ---- X_i
                     const int kb0 = sa + i * kStep;
                     const unsigned char* kt = smem + (i % kStages) * kStageBytes;
-                    const unsigned char* vt = kt + kKvBytes;
-                    // visibility of the 32 keys: the range end, and page validity when
-                    // some page of the sub-range is missing
-                    uint32_t okmask;
-                    if (r.pages_ok) {
-                        const int nin = sbnd - kb0;
-                        okmask = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
-                    } else {
-                        const bool kv_ok = row_of<KVM>(p, r, pages, kb0 + (lane & 31)) >= 0;
-                        okmask = (uint32_t)ballot(kv_ok && lane < 32);
-                    }
                     // S^T = K Q^T for both tiles: the K operand of each 32-dim slice is
                     // read once and used by both (tiles past the token count have a zero
                     // query and no visible key, so they need no branch)
@@ -382,45 +419,31 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                             s1[t] = Tr<DT>::mma(kb[cc], qB[t][cc], s1[t]);
                         }
                     }
-                    // V^T operands (the first kVPre slices read before the softmax, so
-                    // their latency overlaps it; the rest before the P V MFMAs, behind
-                    // the first slices' MFMAs): block lane sl -> key g*4 + sl/4 (+16),
-                    // dims cc*16 + (sl%4)*4;
-                    // row k0 (and k0 + 16), piece (cc*2 + b) ^ ((k0 & 7) << 1), byte hb:
-                    // the swizzle only flips address bits 5-7 of vbase, so slice cc is
-                    // at vbase ^ (32 cc)
-                    const int sl = lane & 15;
-                    const int k0 = g * 4 + (sl >> 2);
-                    const uint32_t vbase = lds_addr(vt) + (uint32_t)(k0 * 256 + 16 * ((sl & 3) >> 1) + (sl & 1) * 8 +
-                                                                     32 * (k0 & 7));
-                    u32x4 va[8];
-                    auto read_v = [&](int cc) {
-                        const u32x2 a0 = lds_read_tr16_at(vbase ^ (uint32_t)(32 * cc));
-                        const u32x2 a1 = lds_read_tr16_at((vbase ^ (uint32_t)(32 * cc)) + 16 * 256);
-                        va[cc] = u32x4{a0[0], a0[1], a1[0], a1[1]};
-                    };
-#pragma unroll
-                    for (int cc = 0; cc < kVPre; ++cc) read_v(cc);
+                    if (i > 0) pv_stage<DT>(vt_prev, pB, tl);
+                    vt_prev = kt + kKvBytes;
                     __builtin_amdgcn_sched_barrier(0);
-                    u32x4 pB[kTiles];
+                    wait_vmcnt<kDmaPerStage * (kAhead - 2)>();  // own share of stage i + 1 landed
+                    wg_barrier();
+                    // ---- Y_i: visibility of the 32 keys (the range end, and page validity
+                    // when some page of the sub-range is missing), then the softmax
+                    uint32_t okmask;
+                    if (r.pages_ok) {
+                        const int nin = sbnd - kb0;
+                        okmask = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
+                    } else {
+                        const bool kv_ok = row_of<KVM>(p, r, pages, kb0 + (lane & 31)) >= 0;
+                        okmask = (uint32_t)ballot(kv_ok && lane < 32);
+                    }
 #pragma unroll
                     for (int t = 0; t < kTiles; ++t) {
                         const int lim = vis_t[t] - kb0;
                         const uint32_t lm = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
                         pB[t] = tile_softmax<DT>(tl[t], s0[t], s1[t], okmask & lm, p.l2scale);
                     }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int cc = kVPre; cc < 8; ++cc) read_v(cc);
-                    // O^T += V^T P^T; each 16-dim slice of V^T serves both tiles
-#pragma unroll
-                    for (int cc = 0; cc < 8; ++cc)
-#pragma unroll
-                        for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va[cc], pB[t], tl[t].o[cc]);
-#pragma unroll
-                    for (int t = 0; t < kTiles; ++t) mfma_settle(tl[t].o);
-                    lds_barrier();  // every wave is done with this stage before it is refilled
+                    issue_stage<KVM>(p, r, pages, ring, i + kAhead, sa + (i + kAhead) * kStep);
                 }
+                if (!grp) wg_barrier();
+                if (nsteps > 0) pv_stage<DT>(vt_prev, pB, tl);
                 wait_vmcnt<0>();    // the trailing zero-row stages land before the ring is reused
                 __syncthreads();
             }

@@ -142,6 +142,31 @@ def test_chunk_causal_block(dv, gpu, dtype):
     close(out, O.paged_sdpa(0.1, **d), dtype, "chunk")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_chunk_page_cache_subranges_and_invalid_pages(dv, gpu, dtype):
+    # S >= 2 (chunk kernel) with one-token pages: a 5000-key view spans three
+    # sub-ranges of the kernel's 2048-entry page-id cache; out-of-pool table
+    # entries (one past the pool, one negative, the latter on a sub-range
+    # boundary) hide their keys
+    W, S, L = 2, 3, 5000
+    loc = np.array([[[4990, 4995, 4999], [3000, 2046, 4500]]], dtype=np.int32)
+    d = rand_paged(1, W, S, 1, 1, [L], 32, dtype, seed=5, loc=loc)
+    bt = d["block_tables"].clone()
+    bt[0, 1234] = d["k_cache"].shape[0]
+    bt[1, 2046] = -5
+    out = run_paged(dv, dict(d, block_tables=bt), 0.1, gpu).cpu()
+    rq = O.rope_q(d["queries"], d["cosines"], d["sines"])[0].float()   # [W,Hq,S,E]
+    hidden = {0: 1234, 1: 2046}
+    for w in range(W):
+        for s in range(S):
+            pos = np.array([j for j in range(min(int(loc[0, w, s]) + 1, L)) if j != hidden[w]])
+            pages = d["block_tables"][w].numpy()[pos]
+            k = d["k_cache"][pages, 0, 0].float()
+            v = d["v_cache"][pages, 0, 0].float()
+            ref = torch.softmax(0.1 * (rq[w, :, s] @ k.T), -1) @ v
+            close(out[w, :, s], ref, dtype, f"w={w} s={s}")
+
+
 def test_paged_through_c_abi_matches_torch_op(dv, gpu):
     from dvattention_amd import capi
     d = rand_paged(2, 4, 1, 8, 16, [300, 220], 128, torch.bfloat16, seed=3)
