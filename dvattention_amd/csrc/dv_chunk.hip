@@ -237,19 +237,26 @@ __device__ inline int loc_of(const DecodeParams& p, int f, int w, int s) {
     return p.loc[((long long)f * p.W + w) * p.S + s];
 }
 
-// Visible keys of a row group: union (max) over its tokens of the per-token count.
+// Length of a row group's key space: per view, the union (max) over its tokens
+// of the view's visible count, summed over views -- the coordinates chunk_piece
+// walks (view f's keys follow the longest range of views 0 .. f-1).  The max
+// over tokens of the per-token sum is shorter whenever different tokens see
+// most in different views, and would leave the tail of the key space unassigned.
 template <int KVM>
 __device__ inline long long group_visible(const DecodeParams& p, int rg) {
     const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
     const int w = rg / nsb, sb = rg - (rg / nsb) * nsb;
     const int s1 = (sb + 1) * kTokBlk < p.S ? (sb + 1) * kTokBlk : p.S;
-    long long best = 0;
-    for (int s = sb * kTokBlk; s < s1; ++s) {
-        long long v = 0;
-        for (int f = 0; f < p.F; ++f) v += view_vis<KVM>(p, f, loc_of(p, f, w, s));
-        best = v > best ? v : best;
+    long long total = 0;
+    for (int f = 0; f < p.F; ++f) {
+        int best = 0;
+        for (int s = sb * kTokBlk; s < s1; ++s) {
+            const int v = view_vis<KVM>(p, f, loc_of(p, f, w, s));
+            best = v > best ? v : best;
+        }
+        total += best;
     }
-    return best;
+    return total;
 }
 
 // O^T += V^T P^T of one stage for both tiles: block lane sl -> key g*4 + sl/4

@@ -143,6 +143,17 @@ def test_chunk_causal_block(dv, gpu, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_chunk_views_longest_for_different_tokens(dv, gpu, dtype):
+    # token 0 sees all of view 0 and little of view 1, token 1 the reverse: the
+    # row group's key space is the per-view union summed over views (3000 keys),
+    # longer than either token's own total
+    loc = np.array([[[1199, 10]], [[20, 1799]]], dtype=np.int32)       # [F=2, W=1, S=2]
+    d = rand_paged(2, 1, 2, 2, 16, [1200, 1800], 64, dtype, seed=9, loc=loc)
+    out = run_paged(dv, d, 0.1, gpu)
+    close(out, O.paged_sdpa(0.1, **d), dtype, "views")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_chunk_page_cache_subranges_and_invalid_pages(dv, gpu, dtype):
     # S >= 2 (chunk kernel) with one-token pages: a 5000-key view spans three
     # sub-ranges of the kernel's 2048-entry page-id cache; out-of-pool table
@@ -322,6 +333,7 @@ def test_varlen_many_rows_multi_launch(dv, gpu):
     (2, 3, 2, 2, [100, 37], [3, 1]),
     (3, 2, 1, 1, [16, 0, 90], [0, 2, 2]),        # 0: 3-D fragment
     (20, 2, 1, 1, [5 + 3 * i for i in range(20)], [2] * 20),   # F > 16: device fragment table
+    (2, 2, 16, 1, [1500, 2500], [2, 0]),          # a full 16-token block, several pieces per segment
 ])
 def test_sdpa_and_fused_vs_oracle(dv, gpu, dtype, F, W, S, Hkv, Ls, batch):
     g = torch.Generator().manual_seed(F * 100 + W)
