@@ -117,6 +117,7 @@ PAGED_CASES = [
     (1, 2, 16, 2, 16, [600], 32),
     (2, 1, 17, 1, 16, [90, 300], 128),
     (1, 3, 5, 8, 64, [700], 64),
+    (1, 1, 3, 16, 16, [200], 64),        # 16 KV heads (256 query heads)
 ]
 
 
@@ -334,6 +335,7 @@ def test_varlen_many_rows_multi_launch(dv, gpu):
     (3, 2, 1, 1, [16, 0, 90], [0, 2, 2]),        # 0: 3-D fragment
     (20, 2, 1, 1, [5 + 3 * i for i in range(20)], [2] * 20),   # F > 16: device fragment table
     (2, 2, 16, 1, [1500, 2500], [2, 0]),          # a full 16-token block, several pieces per segment
+    (18, 2, 3, 1, [40 + 7 * i for i in range(18)], [2] * 18),  # multi-query rows over the device fragment table
 ])
 def test_sdpa_and_fused_vs_oracle(dv, gpu, dtype, F, W, S, Hkv, Ls, batch):
     g = torch.Generator().manual_seed(F * 100 + W)
