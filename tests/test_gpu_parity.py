@@ -113,6 +113,8 @@ PAGED_CASES = [
     (1, 2, 2, 1, 64, [300], 0),
     (2, 1, 4, 2, 1, [20, 9], 16),
     (4, 2, 1, 3, 8, [15, 64, 1, 40], 64),
+    (6, 2, 1, 2, 16, [10, 50, 0, 33, 80, 7], 64),        # more views than one multi-view piece streams
+    (70, 2, 1, 1, 4, [3 + i % 5 for i in range(70)], 32),  # more views than a wave has lanes
     # multi-query rows (S >= 2 takes the chunk kernel for 16-bit types)
     (1, 2, 16, 2, 16, [600], 32),
     (2, 1, 17, 1, 16, [90, 300], 128),
@@ -292,6 +294,7 @@ VARLEN_CASES = [
     (2, 3, 7, [0, 2, 2, 7], 1, 8, [40, 90], 128),
     (3, 3, 6, [0, 4, 2, 5], 2, 16, [20, 6, 33], 32),      # malformed cu_seqlens_q
     (1, 2, 3, [0, 1, 2], 1, 3, [50], 0),
+    (6, 2, 3, [0, 2, 3], 2, 16, [40, 0, 90, 17, 64, 5], 64),
 ]
 
 
