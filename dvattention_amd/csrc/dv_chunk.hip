@@ -123,10 +123,10 @@ struct Tile {
 // Online softmax of one tile for one 32-key stage (softmax32); returns the P^T
 // MFMA operand.
 template <int DT>
-__device__ inline u32x4 tile_softmax(Tile& t, const f32x4& s0, const f32x4& s1, uint32_t mask, float l2scale) {
+__device__ inline POperand tile_softmax(Tile& t, const f32x4& s0, const f32x4& s1, uint32_t mask, float l2scale) {
     float pr[8];
-    softmax32(t.o, t.m, t.l, s0, s1, mask, l2scale, pr);
-    return u32x4{pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]), pack2<DT>(pr[6], pr[7])};
+    softmax32<false>(t.o, t.m, t.l, s0, s1, mask, l2scale, pr);
+    return p_operands<DT>(pr, t.l);
 }
 
 // Query tiles of this wave's tokens for view f, staged through LDS (the K/V ring
@@ -265,7 +265,7 @@ __device__ inline long long group_visible(const DecodeParams& p, int rg) {
 // slice cc is at vbase ^ (32 cc).  Each 16-dim slice of V^T is read once for both
 // tiles; all sixteen reads are issued before the first MFMA.
 template <int DT>
-__device__ inline void pv_stage(const unsigned char* vt, const u32x4 (&pB)[kTiles], Tile (&tl)[kTiles]) {
+__device__ inline void pv_stage(const unsigned char* vt, const POperand (&pB)[kTiles], Tile (&tl)[kTiles]) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, sl = lane & 15;
     const int k0 = g * 4 + (sl >> 2);
@@ -282,7 +282,12 @@ __device__ inline void pv_stage(const unsigned char* vt, const u32x4 (&pB)[kTile
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc)
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va[cc], pB[t], tl[t].o[cc]);
+        for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va[cc], pB[t].hi, tl[t].o[cc]);
+    if constexpr (DT == kF16)
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc)
+#pragma unroll
+            for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va[cc], pB[t].lo, tl[t].o[cc]);
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) mfma_settle(tl[t].o);
 }
@@ -386,7 +391,7 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                 // not execute with an empty exec mask in the other group's waves)
                 const int grp = __builtin_amdgcn_readfirstlane(wv >> 2);
                 const unsigned char* vt_prev = smem;  // V tile of the previous stage
-                u32x4 pB[kTiles] = {};                 // its P^T operands
+                POperand pB[kTiles] = {};              // its P^T operands
                 // prologue: stages 0 .. kAhead-1 (past the end: rows of zeros)
 #pragma unroll
                 for (int st = 0; st < kAhead; ++st) issue_stage<KVM>(p, r, pages, ring, st, sa + st * kStep);

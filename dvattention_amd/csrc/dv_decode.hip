@@ -617,12 +617,14 @@ __device__ inline void compute(SoftState& st, const unsigned char* kt, const uns
         }
     }
     float pr[8];
-    softmax_step(st, s0, s1, mask, l2scale, pr);
+    softmax32<false>(st.o, st.m, st.l, s0, s1, mask, l2scale, pr);
     // P^T operand: k = g*8 + jj <-> key (jj/4)*16 + g*4 + jj%4
-    const u32x4 pB = {pack2<DT>(pr[0], pr[1]), pack2<DT>(pr[2], pr[3]), pack2<DT>(pr[4], pr[5]),
-                      pack2<DT>(pr[6], pr[7])};
+    const POperand pB = p_operands<DT>(pr, st.l);
 #pragma unroll
-    for (int cc = 0; cc < 8; ++cc) st.o[cc] = Tr<DT>::mma(vA[cc], pB, st.o[cc]);
+    for (int cc = 0; cc < 8; ++cc) st.o[cc] = Tr<DT>::mma(vA[cc], pB.hi, st.o[cc]);
+    if constexpr (DT == kF16)
+#pragma unroll
+        for (int cc = 0; cc < 8; ++cc) st.o[cc] = Tr<DT>::mma(vA[cc], pB.lo, st.o[cc]);
     mfma_settle(st.o);
 }
 

@@ -191,6 +191,10 @@ constexpr float kMaxSlack = 8.0f;
 // row with no key yet, m = -inf) takes the exact path, which raises the max to
 // the rows' maximum.  The accumulators are rescaled at one site, so the register
 // allocator keeps them in place across the paths.
+//
+// kSum = false leaves the row sum to the caller (p_operands, for the 16-bit
+// kernels).
+template <bool kSum = true>
 __device__ inline void softmax32(f32x4 (&o)[8], float& m, float& l, const f32x4& s0, const f32x4& s1,
                                  uint32_t mask, float l2scale, float (&pr)[8]) {
     const bool full = mask == 0xffffffffu && l2scale > 0.0f;
@@ -248,10 +252,59 @@ __device__ inline void softmax32(f32x4 (&o)[8], float& m, float& l, const f32x4&
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(pr[i]);
-    float ps = pr[0];
+    if (kSum) {
+        float ps = pr[0];
 #pragma unroll
-    for (int i = 1; i < 8; ++i) ps += pr[i];
-    l += ps;
+        for (int i = 1; i < 8; ++i) ps += pr[i];
+        l += ps;
+    }
+}
+
+// P^T operands of a lane's 8 probabilities, and their row-sum contribution.
+// bf16: one operand; the normaliser sums the rounded weights (v_dot2 with ones,
+// products exact), so the output is a convex combination of V rows -- a softmax
+// concentrated on one key returns that row exactly, where an fp32 normaliser
+// would leave the weight's 2^-9 rounding error.  fp16: the rounding residual
+// p - fp16(p) goes into a second operand (hi + lo carries ~22 bits, one more
+// P V MFMA per slice), so fp16 outputs keep the fp32-P accuracy their 1e-3
+// tolerance needs; the normaliser is the fp32 sum.
+struct POperand {
+    u32x4 hi, lo;  // lo: fp16 only
+};
+
+template <int DT>
+__device__ inline float dot2_ones(uint32_t x, float c) {
+    if constexpr (DT == kBF16)
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, x), __builtin_bit_cast(bf16x2, 0x3f803f80u),
+                                               c, false);
+    else
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, x), __builtin_bit_cast(f16x2, 0x3c003c00u), c, false);
+}
+
+template <int DT>
+__device__ inline POperand p_operands(const float (&pr)[8], float& l) {
+    // the packed words are handled as scalars: taking them as elements of the
+    // vector operand was compiled into four dot products of the first element
+    uint32_t w[4], r[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) w[i] = pack2<DT>(pr[2 * i], pr[2 * i + 1]);
+    if constexpr (DT == kBF16) {
+        float ps = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ps = dot2_ones<DT>(w[i], ps);
+        l += ps;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const f16x2 h = __builtin_bit_cast(f16x2, w[i]);
+            r[i] = pack2<DT>(pr[2 * i] - (float)h[0], pr[2 * i + 1] - (float)h[1]);
+        }
+        float ps = pr[0];
+#pragma unroll
+        for (int i = 1; i < 8; ++i) ps += pr[i];
+        l += ps;
+    }
+    return POperand{u32x4{w[0], w[1], w[2], w[3]}, u32x4{r[0], r[1], r[2], r[3]}};
 }
 
 // ---- query rotation ---------------------------------------------------------
