@@ -15,7 +15,7 @@ from test_gpu_parity import close, hf_cs, rand_paged, rand_varlen, run_paged, ru
 pytestmark = pytest.mark.gpu
 
 DT = [torch.float32, torch.float16, torch.bfloat16]
-CASES = 24
+CASES = 40
 
 
 @pytest.fixture(scope="module")
@@ -27,7 +27,7 @@ def dv(gpu):
 def draw(seed):
     rng = np.random.default_rng(1000 + seed)
     F = int(rng.choice([1, 1, 2, 3, 4, 6]))
-    lens = [int(x) for x in rng.choice([0, 1, 7, 31, 32, 33, 100, 257, 600], size=F)]
+    lens = [int(x) for x in rng.choice([0, 1, 7, 31, 32, 33, 100, 257, 600, 2100], size=F)]
     if max(lens) == 0:
         lens[0] = 50
     return rng, F, lens, DT[int(rng.integers(0, 3))], int(rng.choice([1, 2, 3]))
