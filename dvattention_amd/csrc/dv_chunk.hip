@@ -12,12 +12,15 @@
 //  * K/V pages stream through a 6-stage LDS ring filled by direct-to-LDS loads
 //    (global_load_lds_dwordx4): 32 keys x 256 B of K and of V per stage, one
 //    eighth issued by each wave, completion tracked with vmcnt and a workgroup
-//    barrier.  The loads never pass through VGPRs, so five stages (80 KiB) stay
-//    in flight per CU while the waves run MFMA on the current stage.
+//    barrier.  The loads never pass through VGPRs; four stages ahead of the one
+//    computed are in flight per CU.
 //  * Per stage and tile: S^T = K Q^T on 16x16x32 MFMA (8 per tile), online
-//    softmax per query row, O^T += V^T P^T (8 MFMA per tile) with V^T read by
-//    the transposing LDS read; K/V operands are read from LDS once per stage and
-//    reused by the wave's two tiles.
+//    softmax per query row, O^T += V^T P^T (8 MFMA per tile, 16 for fp16: see
+//    p_operands) with V^T read by the transposing LDS read; K/V operands are
+//    read from LDS once per stage and reused by the wave's two tiles.
+//  * Ping-pong: a stage is an MFMA cluster (S of stage i, P V of stage i - 1)
+//    and a softmax cluster, separated by workgroup barriers; the two waves of a
+//    SIMD run one cluster apart, so one's softmax overlaps the other's MFMAs.
 //  * Rows are causal-masked per token (key l visible iff l <= locations[f,w,s]).
 //  * The balanced split / LSE merge is the decode kernel's (equal key chunks per
 //    workgroup, fp32 partial slots, dv_merge_chunk).
