@@ -1,9 +1,13 @@
 """GPU parity of the HIP kernels against the CPU oracle (marked ``gpu``).
 
 Tolerances (max-abs against the fp32 oracle): fp32 1e-5, fp16 1e-3, bf16 2e-2.
-The query rotation is compared bit-exactly; page-table / varlen indexing is
-checked bit-exactly through GPU-vs-GPU identities (page permutation, split
-invariance) and exact special cases.
+Where one unit in the last place of the 16-bit output itself exceeds the
+tolerance (fp16 outputs of magnitude >= 2, bf16 >= 4: their rounding alone can
+be 0.98e-3 / 1.6e-2 or more), an element that misses the tolerance must instead
+lie within one unit of the oracle value rounded to the output type -- no 16-bit
+output can do better there.  The query rotation is compared bit-exactly;
+page-table / varlen indexing is checked bit-exactly through GPU-vs-GPU
+identities (page permutation, split invariance) and exact special cases.
 """
 import numpy as np
 import pytest
@@ -25,10 +29,28 @@ def hf_cs(pos, R, base=1e4):
     return torch.from_numpy(np.cos(emb).astype(np.float32)), torch.from_numpy(np.sin(emb).astype(np.float32))
 
 
+MANT = {torch.float16: 10, torch.bfloat16: 7}
+
+
+def ulp16(x, dtype):
+    """Unit in the last place of the 16-bit ``dtype`` at the (rounded) values x."""
+    a = x.abs().clamp_min(torch.finfo(dtype).tiny)
+    return torch.exp2(torch.floor(torch.log2(a)) - MANT[dtype])
+
+
 def close(gpu_out, ref, dtype, what=""):
-    err = (gpu_out.float().cpu() - ref.float()).abs().max().item() if ref.numel() else 0.0
-    assert err <= TOL[dtype], f"{what}: max-abs error {err} > {TOL[dtype]} ({dtype})"
-    return err
+    if not ref.numel():
+        return 0.0
+    g, r = gpu_out.float().cpu(), ref.float()
+    err = (g - r).abs()
+    miss = err > TOL[dtype]
+    if miss.any() and dtype in MANT:
+        rr = r.to(dtype).float()
+        u = ulp16(rr, dtype)
+        miss &= (u <= TOL[dtype]) | ((g - rr).abs() > u)
+    assert not miss.any(), (f"{what}: max-abs error {err.max().item()} > {TOL[dtype]} ({dtype}) at "
+                            f"{int(miss.sum())} elements, e.g. |ref| {r[miss].abs().max().item():.3f}")
+    return err.max().item()
 
 
 @pytest.fixture(scope="module")
@@ -143,6 +165,16 @@ def test_chunk_causal_block(dv, gpu, dtype):
     d = rand_paged(1, W, S, Hkv, bs, [L], 32, dtype, seed=21, loc=loc)
     out = run_paged(dv, d, 0.1, gpu)
     close(out, O.paged_sdpa(0.1, **d), dtype, "chunk")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_chunk_many_row_groups_multi_launch(dv, gpu, dtype):
+    # 2100 sequences x 2 tokens: more 16-token row groups than one launch's
+    # schedule holds (2048), so the rows are split over two launches that reuse
+    # the workspace
+    d = rand_paged(1, 2100, 2, 1, 16, [40], 32, dtype, seed=13)
+    out = run_paged(dv, d, 0.1, gpu)
+    close(out, O.paged_sdpa(0.1, **d), dtype, "multi-launch chunk")
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])

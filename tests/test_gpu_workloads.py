@@ -2,17 +2,16 @@
 the inputs bench.py times): the HIP output of sampled rows against the CPU
 oracle run on just those rows (their queries, locations, cos/sin and the pages
 their block tables name, remapped into a compact cache), and a second call
-bit-identical to the first.  Tolerances as in test_gpu_parity.
+bit-identical to the first.  Tolerance rule of test_gpu_parity.close.
 """
 import numpy as np
 import pytest
 import torch
 
 from oracle import dvattn_oracle as O
+from test_gpu_parity import close
 
 pytestmark = pytest.mark.gpu
-
-TOL = {torch.float32: 1e-5, torch.float16: 1e-3, torch.bfloat16: 2e-2}
 
 
 def compact_pages(t, rows, dev):
@@ -45,11 +44,6 @@ def varlen_rows(wl, rows, dev):
                 cu_seqlens_k=torch.zeros(n + 1, dtype=torch.int32))
 
 
-def check(out, ref, dtype, what):
-    err = (out.float().cpu() - ref.float()).abs().max().item()
-    assert err <= TOL[dtype], f"{what}: max-abs error {err} > {TOL[dtype]}"
-
-
 @pytest.mark.parametrize("cfg,rows", [(1, None), (2, [0, 13, 31]), (3, [0, 5, 40, 63]), (4, [2]), (5, [0, 11])])
 def test_config_rows_vs_oracle(gpu, cfg, rows):
     from dvattention_amd import workloads as WL
@@ -64,10 +58,10 @@ def test_config_rows_vs_oracle(gpu, cfg, rows):
         ref, _ = O.fused(wl.scale, t["locations"].cpu(), t["queries"].cpu(), t["fragment_lengths"].cpu(),
                          [k.cpu() for k in t["keys"]], [v.cpu() for v in t["values"]], t["cosines"].cpu(),
                          t["sines"].cpu())
-        check(out, ref, wl.dtype, f"config {cfg}")
+        close(out, ref, wl.dtype, f"config {cfg}")
     elif wl.op == "paged":
         ref = O.paged_sdpa(wl.scale, **paged_rows(wl, rows, gpu))
-        check(out[torch.tensor(rows).to(gpu)], ref, wl.dtype, f"config {cfg} rows {rows}")
+        close(out[torch.tensor(rows).to(gpu)], ref, wl.dtype, f"config {cfg} rows {rows}")
     else:
         ref = O.varlen_paged_sdpa(wl.scale, **varlen_rows(wl, rows, gpu))
-        check(out[torch.tensor(rows).to(gpu)], ref, wl.dtype, f"config {cfg} rows {rows}")
+        close(out[torch.tensor(rows).to(gpu)], ref, wl.dtype, f"config {cfg} rows {rows}")
