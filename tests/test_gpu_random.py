@@ -132,3 +132,35 @@ def test_random_kv_append(dv, gpu, seed):
     what = f"seed {seed}: W={W} S={S} Hkv={Hkv} bs={bs} maxB={maxB} R={R} {dtype} cos {c.dtype}"
     assert torch.equal(kg.cpu(), k_ref), "K cache differs, " + what
     assert torch.equal(vg.cpu(), v_ref), "V cache differs, " + what
+
+
+@pytest.mark.parametrize("seed", range(CASES // 2))
+def test_random_view_metadata(dv, gpu, seed):
+    """View locations bit-exact and cos/sin within the trigonometric tolerance of
+    test_gpu_cache: random segment counts, lengths, per-sequence orders (with
+    missing, repeated and padding entries), token counts, rotary widths, scaling
+    and rounding."""
+    from test_gpu_cache import TRIG_TOL
+    rng = np.random.default_rng(7000 + seed)
+    F, W, S = int(rng.integers(1, 7)), int(rng.integers(1, 6)), int(rng.integers(1, 5))
+    R = int(rng.choice([16, 64, 128]))
+    lens = [int(x) for x in rng.integers(0, 70000, size=F)]
+    order = np.stack([rng.permutation(F) for _ in range(W)]).astype(np.int32)
+    for w in range(W):
+        if F > 1 and rng.random() < 0.3:
+            order[w, int(rng.integers(0, F))] = int(rng.choice([-1, order[w, 0]]))
+    scaling = float(rng.choice([1.0, 0.9, 1.3]))
+    round_to = [None, torch.bfloat16, torch.float16][int(rng.integers(0, 3))]
+    base = float(rng.choice([1e4, 5e5]))
+    inv_freq = (1.0 / (base ** (torch.arange(0, R, 2, dtype=torch.float) / R))).float()
+    loc_r, cos_r, sin_r = O.view_metadata(lens, order.tolist(), S, inv_freq, scaling, round_to)
+    loc, cos, sin = dv.dvattn_view_metadata(torch.tensor(lens, dtype=torch.int32, device=gpu),
+                                            torch.from_numpy(order).to(gpu), S, inv_freq.to(gpu), scaling, round_to)
+    what = f"seed {seed}: F={F} W={W} S={S} R={R} lens={lens} scaling={scaling} round_to={round_to}"
+    assert torch.equal(loc.cpu(), loc_r), "locations differ, " + what
+    dc, ds = (cos.cpu() - cos_r).abs(), (sin.cpu() - sin_r).abs()
+    if round_to is None:
+        assert dc.max().item() <= TRIG_TOL * scaling and ds.max().item() <= TRIG_TOL * scaling, what
+    else:   # one step of the 16-bit type where the fp32 values straddle a rounding boundary
+        step = 2 ** -8 if round_to == torch.bfloat16 else 2 ** -11
+        assert dc.max().item() <= step * scaling * 2 and ds.max().item() <= step * scaling * 2, what
