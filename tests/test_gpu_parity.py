@@ -1,14 +1,20 @@
 """GPU parity of the HIP kernels against the CPU oracle (marked ``gpu``).
 
 Tolerances (max-abs against the fp32 oracle): fp32 1e-5, fp16 1e-3, bf16 2e-2.
-Where one unit in the last place of the 16-bit output itself exceeds the
-tolerance (fp16 outputs of magnitude >= 2, bf16 >= 4: their rounding alone can
-be 0.98e-3 / 1.6e-2 or more), an element that misses the tolerance must instead
-lie within one unit of the oracle value rounded to the output type -- no 16-bit
-output can do better there.  The query rotation is compared bit-exactly;
-page-table / varlen indexing is checked bit-exactly through GPU-vs-GPU
-identities (page permutation, split invariance) and exact special cases.
+A correctly rounded 16-bit output misses the tolerance only where half a unit
+in the last place of the output type exceeds it: fp16 outputs of magnitude
+>= 4 (half ulp 1.95e-3) and bf16 >= 8 (half ulp 3.1e-2).  There, and only
+there, an element may miss the tolerance by at most that half ulp (error <=
+tolerance + half ulp: the fp32 result within tolerance, then rounded once).
+Below those magnitudes every element must meet the tolerance outright.  Each
+call records how many elements took the half-ulp allowance (``FORGIVEN``);
+the session summary prints the counts.  The query rotation is compared
+bit-exactly; page-table / varlen indexing is checked bit-exactly through
+GPU-vs-GPU identities (page permutation, split invariance) and exact special
+cases.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -19,6 +25,9 @@ pytestmark = pytest.mark.gpu
 
 TOL = {torch.float32: 1e-5, torch.float16: 1e-3, torch.bfloat16: 2e-2}
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
+
+# test node id -> [elements checked, elements that took the half-ulp allowance]
+FORGIVEN = {}
 
 
 def hf_cs(pos, R, base=1e4):
@@ -39,16 +48,30 @@ def ulp16(x, dtype):
 
 
 def close(gpu_out, ref, dtype, what=""):
+    """Max-abs check of ``gpu_out`` against the fp32 oracle ``ref`` under the
+    rule in the module docstring; returns the max-abs error."""
     if not ref.numel():
         return 0.0
     g, r = gpu_out.float().cpu(), ref.float()
     err = (g - r).abs()
-    miss = err > TOL[dtype]
+    tol = TOL[dtype]
+    miss = err > tol
+    forgiven = 0
     if miss.any() and dtype in MANT:
         rr = r.to(dtype).float()
-        u = ulp16(rr, dtype)
-        miss &= (u <= TOL[dtype]) | ((g - rr).abs() > u)
-    assert not miss.any(), (f"{what}: max-abs error {err.max().item()} > {TOL[dtype]} ({dtype}) at "
+        # half an ulp of the output type exceeds the tolerance at the rounded
+        # reference value; the allowance is half an ulp of the larger magnitude
+        # of output and rounded reference (a result rounded across a binade edge)
+        arm = ulp16(rr, dtype) / 2 > tol
+        allow = tol + ulp16(torch.maximum(g.abs(), rr.abs()), dtype) / 2
+        ok = miss & arm & (err <= allow)
+        forgiven = int(ok.sum())
+        miss &= ~ok
+    key = os.environ.get("PYTEST_CURRENT_TEST", "?").split(" ")[0]
+    rec = FORGIVEN.setdefault(key, [0, 0])
+    rec[0] += err.numel()
+    rec[1] += forgiven
+    assert not miss.any(), (f"{what}: max-abs error {err[miss].max().item()} > {tol} ({dtype}) at "
                             f"{int(miss.sum())} elements, e.g. |ref| {r[miss].abs().max().item():.3f}")
     return err.max().item()
 
