@@ -24,7 +24,7 @@ STATUS = {0: "DVATTN_OK", 1: "DVATTN_ERR_INVALID", 2: "DVATTN_ERR_UNSUPPORTED", 
 # Every function include/dvattn_amd.h declares.
 EXPORTED = [
     "dvattn_last_error", "dvattn_abi_version",
-    "dvattn_paged_sdpa_workspace_size", "dvattn_paged_sdpa",
+    "dvattn_paged_sdpa_workspace_size", "dvattn_paged_sdpa", "dvattn_paged_sdpa_noalloc",
     "dvattn_varlen_paged_sdpa_workspace_size", "dvattn_varlen_paged_sdpa",
     "dvattn_sdpa_workspace_size", "dvattn_sdpa", "dvattn_fused",
     "dvattn_rope", "dvattn_varlen_rope",
@@ -78,6 +78,8 @@ def lib() -> ctypes.CDLL:
             getattr(L, n).argtypes = [_I, _SP, _I]
         L.dvattn_paged_sdpa.restype = _I
         L.dvattn_paged_sdpa.argtypes = [_I, _VP, _F, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SP, _VP, _SZ, _VP]
+        L.dvattn_paged_sdpa_noalloc.restype = _I
+        L.dvattn_paged_sdpa_noalloc.argtypes = [_I, _VP, _F, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SP, _VP]
         L.dvattn_varlen_paged_sdpa.restype = _I
         L.dvattn_varlen_paged_sdpa.argtypes = [_I, _VP, _F, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _SP,
                                                _VP, _SZ, _VP]
@@ -138,6 +140,21 @@ def paged_sdpa(out, scale, locations, queries, cosines, sines, fragment_lengths,
                                _ptr(fragment_lengths), _ptr(k_cache), _ptr(v_cache), _ptr(block_tables),
                                ctypes.byref(s), _ptr(ws), ws.numel(), _stream(out)))
     return out
+
+
+def paged_sdpa_noalloc(out, scale, locations, queries, cosines, sines, fragment_lengths, k_cache, v_cache,
+                       block_tables, shape: Shape | None = None) -> torch.Tensor:
+    """dvattn_paged_sdpa_noalloc: dvattn_paged_sdpa on the library's static
+    per-GPU scratch (no workspace argument, nothing allocated)."""
+    L = lib()
+    s = shape or paged_shape(queries, locations, cosines, k_cache, v_cache, block_tables)
+    _check(L.dvattn_paged_sdpa_noalloc(dtype_code(out.dtype), _ptr(out), scale, _ptr(locations), _ptr(queries),
+                                       _ptr(cosines), _ptr(sines), _ptr(fragment_lengths), _ptr(k_cache),
+                                       _ptr(v_cache), _ptr(block_tables), ctypes.byref(s), _stream(out)))
+    return out
+
+
+NOALLOC_SCRATCH_BYTES = 64 << 20   # DVATTN_NOALLOC_SCRATCH_BYTES
 
 
 def varlen_paged_sdpa(out, scale, locations, queries, cosines, sines, fragment_lengths, k_cache, v_cache,

@@ -6,6 +6,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <vector>
 
 #include "../../include/dvattn_amd.h"
@@ -78,6 +79,38 @@ dvattn_status check_pages(const dvattn_shape* s) {
 }
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// ---- static scratch of dvattn_paged_sdpa_noalloc ------------------------------
+// Device memory for the partial results and merge directory of the paged entry
+// point, for callers that cannot allocate.  Each GPU the library runs on holds
+// its own copy of the array until the process ends.  In host code `scratch`
+// names a host-side stand-in, never the device memory: the device address is
+// taken once per device with hipGetSymbolAddress and only that address is used.
+constexpr size_t kScratchBytes = (size_t)DVATTN_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_dev[kMaxDevices] = {};
+
+// Device address of `scratch` on the current device (looked up on the first
+// call on that device, with the device current).
+dvattn_status scratch_address(void** out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(DVATTN_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(DVATTN_ERR_UNSUPPORTED, "device %d beyond %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(DVATTN_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+        g_scratch_dev[dev] = ptr;
+    }
+    *out = g_scratch_dev[dev];
+    return DVATTN_OK;
+}
 
 size_t contig_table_bytes(int F) {
     return F > dv::kMaxFragArgs ? align256((size_t)F * sizeof(dv::FragDesc)) : 0;
@@ -154,6 +187,27 @@ dvattn_status dvattn_paged_sdpa(int dtype, void* out, float scale, const int* lo
     }
     if (e != hipSuccess) return hip_fail(e, "dvattn_paged_sdpa launch");
     return ok();
+}
+
+dvattn_status dvattn_paged_sdpa_noalloc(int dtype, void* out, float scale, const int* locations,
+                                        const void* queries, const float* cosines, const float* sines,
+                                        const int* fragment_lengths, const void* k_cache, const void* v_cache,
+                                        const int* block_tables, const dvattn_shape* s, void* stream) {
+    if (!s) return fail(DVATTN_ERR_INVALID, "shape is null");
+    if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
+    const size_t need = dvattn_paged_sdpa_workspace_size(dtype, s, -1);
+    if (need > kScratchBytes)
+        return fail(DVATTN_ERR_WORKSPACE,
+                    "dvattn_paged_sdpa_noalloc: this shape needs %zu bytes of scratch, the static scratch "
+                    "holds %zu (use dvattn_paged_sdpa with a workspace)",
+                    need, kScratchBytes);
+    void* ws = nullptr;
+    const dvattn_status st = scratch_address(&ws);
+    if (st != DVATTN_OK) return st;
+    // nothing in the scratch has to start at zero: every call's kernels write the
+    // partial slots and the merge directory before reading them
+    return dvattn_paged_sdpa(dtype, out, scale, locations, queries, cosines, sines, fragment_lengths, k_cache,
+                             v_cache, block_tables, s, ws, kScratchBytes, stream);
 }
 
 // ---------------------------------------------------------------------------

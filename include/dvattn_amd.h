@@ -113,6 +113,24 @@ DVATTN_API dvattn_status dvattn_paged_sdpa(int dtype, void* out, float scale, co
                                 const int* block_tables, const dvattn_shape* shape,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- paged decode attention without allocation -----------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  Same arguments, checks and results as dvattn_paged_sdpa,
+ * minus the workspace: the partial results and merge directory live in a static
+ * device array of DVATTN_NOALLOC_SCRATCH_BYTES that each GPU the library runs on
+ * holds until the process ends.  A shape whose dvattn_paged_sdpa_workspace_size
+ * exceeds it is rejected with DVATTN_ERR_WORKSPACE.  The call allocates nothing
+ * (no hipMalloc, no allocating library routine).  Every call on a GPU uses that
+ * GPU's one array: calls that overlap on one GPU (two streams or threads at
+ * once) race and must be serialised by the caller. */
+#define DVATTN_NOALLOC_SCRATCH_BYTES (64u << 20)
+DVATTN_API dvattn_status dvattn_paged_sdpa_noalloc(int dtype, void* out, float scale, const int* locations,
+                                        const void* queries, const float* cosines, const float* sines,
+                                        const int* fragment_lengths, const void* k_cache,
+                                        const void* v_cache, const int* block_tables,
+                                        const dvattn_shape* shape, void* stream);
+
 /* ---- varlen paged decode attention with fused query RoPE -------------------
  * out [T,Hq,Ev] T; locations [F,T] i32 (a view with locations < 0 is skipped);
  * queries [T,Hq,E] T; cosines/sines [F,T,R/2] f32 (half width);
