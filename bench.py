@@ -222,8 +222,17 @@ def cpu_baseline(device, budget_s: float = 10.0) -> dict:
     median run time gives the rate."""
     from dvattention_amd import workloads as WL
     from oracle import dvattn_oracle as O
-    cores = min(os.cpu_count() or 1, 16)
+    # every core of the host (BASELINE.md's protocol): os.cpu_count(), which on
+    # the MI355X box equals its scheduler affinity and its cgroup CPU quota
+    cores = os.cpu_count() or 1
     torch.set_num_threads(cores)
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else cores
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        quota = None if q == "max" else round(int(q) / int(period), 2)
+    except (OSError, ValueError):
+        pass
     wl = WL.config(2, device="cpu", seed=1234)
     t = wl.t
 
@@ -253,9 +262,11 @@ def cpu_baseline(device, budget_s: float = 10.0) -> dict:
         "unit": "TB/s",
         "cores": cores,
         "kind": "port",
+        "host_cpus": {"cpu_count": os.cpu_count(), "affinity": avail, "cgroup_quota": quota,
+                      "model": cpu_model or platform.processor()},
         "sample": f"full config 2 input ({wl.alg_bytes / 1e6:.0f} MB algorithmic), median of {len(runs)} runs = "
-                  f"{med * 1e3:.1f} ms/call, fp32 torch-CPU oracle, {cpu_model or platform.processor()}, "
-                  f"torch {torch.__version__}",
+                  f"{med * 1e3:.1f} ms/call, fp32 torch-CPU oracle on {cores} threads, "
+                  f"{cpu_model or platform.processor()}, torch {torch.__version__}",
     }
 
 

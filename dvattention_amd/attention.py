@@ -154,26 +154,51 @@ def dvattn_view_metadata(fragment_lengths: torch.Tensor, order: torch.Tensor, nu
 
 def dvattn_sdpa_pt(queries: torch.Tensor, locations: torch.Tensor, keys: list, values: list,
                    scale: float, return_intermediate_results: bool = False):
-    """The reference's pure-PyTorch debugging helper (attention.py:36-65), kept
-    for API compatibility.  It is not used by any operator of this package."""
-    qk = []
-    vals = []
-    for f in range(len(keys)):
-        key = keys[f].repeat_interleave(queries.size(-3) // keys[f].size(-3), -3)
-        val = values[f].repeat_interleave(queries.size(-3) // values[f].size(-3), -3)
-        kp = torch.arange(0, key.size(-2), dtype=torch.int32, device=key.device)[None, None, None, :]
-        qp = locations[f][:, None, :, None]
-        mask = kp > qp
-        att = queries[f].to(torch.float32) @ key.transpose(-1, -2).to(torch.float32)
-        att.masked_fill_(mask, float("-inf"))
-        qk.append(att)
-        vals.append(val)
-    qk = torch.concat(qk, dim=-1)
-    vals = torch.concat(vals, dim=-2).to(torch.float32)
-    att = torch.softmax(scale * qk, dim=-1)
-    result = att @ vals
+    """Pure-PyTorch attention over already-rotated queries and contiguous views,
+    for testing and debugging; the reference's helper of the same name and
+    contract (attention.py:36-65).  No operator of this package calls it.
+
+    queries ``[F,W,Hq,S,E]`` (rotated per view), locations ``[F,W,S]``,
+    keys[f] / values[f] ``[B,Hkv,L_f,E|Ev]`` or ``[Hkv,L_f,E|Ev]`` (B = 1
+    broadcasts over the W sequences).  Key ``l`` of view ``f`` is visible to
+    query ``(w, s)`` iff ``l <= locations[f, w, s]``; one fp32 softmax of
+    ``scale * q.k`` runs over the keys of all views.  Returns the output in
+    ``queries.dtype``; with ``return_intermediate_results``, the fp32 output
+    ``[W,Hq,S,Ev]``, the masked unscaled scores and the softmax weights
+    ``[W,Hq,S,sum_f L_f]``.  A query that sees no key gets NaN here (the HIP
+    operators write zeros, as the reference's kernels do).
+
+    GQA without replicating K/V: the 16 query heads of a KV head are viewed as
+    16*S query rows of that head.  The views' scores fill one preallocated
+    key axis, and visibility is one comparison of every key's in-view position
+    against the query's location in that key's view.
+    """
+    F, W, Hq, S, E = queries.shape
+    Hkv = keys[0].shape[-3]
+    G = Hq // Hkv
+    Ev = values[0].shape[-1]
+    dev = queries.device
+    lens = [int(k.shape[-2]) for k in keys]
+    total = sum(lens)
+    view_of = torch.repeat_interleave(torch.arange(F, device=dev), torch.tensor(lens, device=dev))
+    pos_in_view = torch.cat([torch.arange(n, device=dev) for n in lens]) if total else \
+        torch.zeros(0, dtype=torch.long, device=dev)
+
+    scores = torch.empty((W, Hkv, G * S, total), dtype=torch.float32, device=dev)
+    v_all = torch.empty((W, Hkv, total, Ev), dtype=torch.float32, device=dev)
+    start = 0
+    for f, n in enumerate(lens):
+        q_rows = queries[f].to(torch.float32).reshape(W, Hkv, G * S, E)
+        scores[..., start:start + n] = q_rows @ keys[f].to(torch.float32).transpose(-1, -2)
+        v_all[:, :, start:start + n] = values[f].to(torch.float32)
+        start += n
+    scores = scores.view(W, Hq, S, total)
+    hidden = pos_in_view > locations.to(device=dev, dtype=torch.long)[view_of].permute(1, 2, 0)  # [W,S,total]
+    scores.masked_fill_(hidden[:, None], float("-inf"))
+    weights = torch.softmax(scores * scale, dim=-1)
+    result = (weights.view(W, Hkv, G * S, total) @ v_all).view(W, Hq, S, Ev)
     if return_intermediate_results:
-        return result, qk, att
+        return result, scores, weights
     return result.to(queries.dtype)
 
 

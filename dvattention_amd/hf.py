@@ -100,6 +100,38 @@ class Segment:
         return self.pool.v[layer_idx][self.index:self.index + 1]
 
 
+def _cache_layer(cache, layer: int):
+    """(keys, values) ``[1, Hkv, L, E]`` of one layer of a transformers cache
+    (``layers[i].keys`` in transformers 5, ``key_cache[i]`` before)."""
+    if hasattr(cache, "layers"):
+        return cache.layers[layer].keys, cache.layers[layer].values
+    return cache.key_cache[layer], cache.value_cache[layer]
+
+
+def segments_from_caches(caches, pool: SegmentPool, first: int = 0) -> List[Segment]:
+    """Copy caller-owned transformers caches into pool segments ``first``,
+    ``first + 1``, ...: the reference's ``DVAttnCache`` takes such caches, one
+    per segment (attention.py:109-119); here each becomes a segment of ``pool``
+    holding the same (already rotated) keys and values, in the cache's own
+    position numbering (the segment's token 0 at position 0).  Returns the
+    segments, for a ``DVAttnCache`` structure."""
+    out = []
+    for j, cache in enumerate(caches):
+        seg = pool[first + j]
+        for layer in range(pool.num_layers):
+            k, v = _cache_layer(cache, layer)
+            if k.dim() != 4 or k.shape[0] != 1:
+                raise ValueError(f"cache {j} layer {layer}: expected keys [1, Hkv, L, E], got {tuple(k.shape)}")
+            L = k.shape[2]
+            if L > pool.capacity:
+                raise RuntimeError(f"cache {j} holds {L} tokens, more than the pool's {pool.capacity}")
+            pool.k[layer][seg.index, :, :L].copy_(k[0])
+            pool.v[layer][seg.index, :, :L].copy_(v[0])
+            seg.lengths[layer] = L
+        out.append(seg)
+    return out
+
+
 class DVAttnCache:
     """Multi-worker dynamic-view cache (attention.py:109-239).
 
@@ -149,13 +181,19 @@ class DVAttnCache:
             # shared by all layers of this step
             n_new = mask.sum(dim=1).tolist() if mask is not None else [S] * W
             pos = torch.full((W, S), -1, dtype=torch.int32)
+            # workers that write to the same segment append one after another,
+            # in worker order (the reference updates their caches in turn,
+            # attention.py:141-152)
+            next_pos = {}
             for w in range(W):
                 n = int(n_new[w])
-                base = self.write_to[w].get_seq_length(0)
+                seg = self.write_to[w]
+                base = next_pos.get(id(seg), seg.get_seq_length(0))
                 if base + n > self.pool.capacity:
-                    raise RuntimeError(f"segment {self.write_to[w].index} is full ({base} + {n} > "
+                    raise RuntimeError(f"segment {seg.index} is full ({base} + {n} > "
                                        f"{self.pool.capacity} tokens)")
                 pos[w, S - n:] = torch.arange(base, base + n, dtype=torch.int32)
+                next_pos[id(seg)] = base + n
             self._n_new = [int(n) for n in n_new]
             self._positions = pos.to(dev, non_blocking=True)
             self._wt_table = torch.tensor([[seg.index] for seg in self.write_to], dtype=torch.int32).to(dev)
@@ -254,7 +292,11 @@ def merge_caches(target: Segment, source: Segment, model, ops=HipOps) -> None:
 
 
 class AttentionModule(nn.Module):
-    """Drop-in self-attention of a transformers decoder layer (attention.py:254-331)."""
+    """Drop-in self-attention of a transformers decoder layer (attention.py:254-331).
+
+    A model configured with ``_attn_implementation == "eager"`` runs the
+    attention in PyTorch (``dvattn_sdpa_pt``, as the reference does at
+    attention.py:309-312); any other setting runs the HIP ``dvattn_fused``."""
 
     def __init__(self, config, layer_idx: int):
         super().__init__()
@@ -285,10 +327,21 @@ class AttentionModule(nn.Module):
         # the key rotation (attention.py:304) happens inside the cache append
         cache = cache_obj.update(key_states, value_states, self.layer_idx,
                                  {"cos": cos, "sin": sin, "mask": attention_mask})
-        rq = cache_obj.get_queries_buffer(query_states, self.layer_idx)
-        out = cache_obj.get_att_buffer(rq, self.layer_idx)
-        cache_obj.ops.fused(query_states, cache.loc, cache.keys, cache.values, self.scaling, cache.frags, cache.cos,
-                            cache.sin, rq, out)
+        if self.config._attn_implementation == "eager":
+            # PyTorch path of the attention (attention.py:309-312): the query
+            # rotated for every view, then one softmax over all views' keys
+            # (each view cut to its filled length; later keys are masked anyway)
+            F = cache.cos.size(0)
+            rq = _A.apply_rotary_pos_emb(query_states[None].expand(F, -1, -1, -1, -1), cache.cos, cache.sin,
+                                         unsqueeze_dim=2)
+            keys = [k[:, :, :seg.get_seq_length(self.layer_idx)] for k, seg in zip(cache.keys, cache_obj.segments)]
+            vals = [v[:, :, :seg.get_seq_length(self.layer_idx)] for v, seg in zip(cache.values, cache_obj.segments)]
+            out = _A.dvattn_sdpa_pt(rq, cache.loc, keys, vals, self.scaling)
+        else:
+            rq = cache_obj.get_queries_buffer(query_states, self.layer_idx)
+            out = cache_obj.get_att_buffer(rq, self.layer_idx)
+            cache_obj.ops.fused(query_states, cache.loc, cache.keys, cache.values, self.scaling, cache.frags,
+                                cache.cos, cache.sin, rq, out)
         attn_output = out.transpose(1, 2).reshape(*input_shape, -1).contiguous()
         return self.o_proj(attn_output), None
 
@@ -305,4 +358,4 @@ def model_surgery(model) -> None:
 
 
 __all__ = ["CacheStructure", "SegmentPool", "Segment", "DVAttnCache", "merge_caches", "AttentionModule",
-           "model_surgery", "HipOps"]
+           "model_surgery", "HipOps", "segments_from_caches"]

@@ -421,6 +421,30 @@ def test_sdpa_and_fused_vs_oracle(dv, gpu, dtype, F, W, S, Hkv, Ls, batch):
     assert torch.equal(out2, out)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("S", [1, 3])
+def test_sdpa_fragment_lengths_below_tensor_length(dv, gpu, dtype, S):
+    # fragment_lengths[f] < L_f (a preallocated cache that is only partly
+    # filled, as the model integration's segments are): view f's keys are the
+    # first fragment_lengths[f] rows of each (batch, head) of the [B,Hkv,L_f,E]
+    # tensor -- the tensor's own strides -- so the result equals the same call
+    # on the tensors cut to those rows, and the oracle (contig_sdpa) agrees
+    F, W, Hkv = 3, 2, 2
+    Ls, fl = [300, 90, 64], [211, 90, 1]
+    g = torch.Generator().manual_seed(77 + S)
+    keys = [torch.randn(W, Hkv, L, 128, generator=g).to(dtype) for L in Ls]
+    vals = [torch.randn(W, Hkv, L, 128, generator=g).to(dtype) for L in Ls]
+    loc = torch.tensor(np.random.default_rng(S).integers(0, 300, size=(F, W, S)), dtype=torch.int32)
+    q = torch.randn(F, W, 16 * Hkv, S, 128, generator=g).to(dtype)
+    flt = torch.tensor(fl, dtype=torch.int32)
+    out = dv.dvattn_sdpa(q.to(gpu), loc.to(gpu), [k.to(gpu) for k in keys], [v.to(gpu) for v in vals], 0.1,
+                         flt.to(gpu))
+    cut = dv.dvattn_sdpa(q.to(gpu), loc.to(gpu), [k[:, :, :n].contiguous().to(gpu) for k, n in zip(keys, fl)],
+                         [v[:, :, :n].contiguous().to(gpu) for v, n in zip(vals, fl)], 0.1, flt.to(gpu))
+    assert torch.equal(out, cut)
+    close(out, O.contig_sdpa(0.1, loc, q, flt, keys, vals), dtype, "fragment_lengths < L")
+
+
 def test_fused_through_c_abi(gpu):
     from dvattention_amd import capi
     q = torch.randn(1, 16, 1, 128)

@@ -63,12 +63,17 @@ def tiny_qwen2(dtype, device, seed=0):
     return m.to(device=device, dtype=dtype)
 
 
-def surgery_copy(model, device=None, dtype=None):
+def surgery_copy(model, device=None, dtype=None, attn="sdpa"):
+    """A copy of ``model`` with DVAttn attention; ``attn`` is the configured
+    attention implementation ("eager" selects the module's PyTorch path, any
+    other the ``ops.fused`` path)."""
     from dvattention_amd import hf
     m = copy.deepcopy(model)
     if device is not None:
         m = m.to(device=device, dtype=dtype)
+    m.config._attn_implementation = attn
     hf.model_surgery(m)
+    assert m.model.layers[0].self_attn.config._attn_implementation == attn
     return m
 
 
@@ -156,6 +161,84 @@ def test_cache_positions_and_views_cpu():
     assert torch.all(pool.k[0][1, :, 2:] == 0)  # nothing past the two real tokens
 
 
+def test_eager_module_matches_transformers_cpu():
+    """_attn_implementation == "eager": the module's PyTorch attention
+    (dvattn_sdpa_pt over per-view rotated queries) on the oracle cache ops
+    decodes like transformers' own attention."""
+    model = tiny_qwen2(torch.float32, "cpu")
+    ours = surgery_copy(model, attn="eager")
+    prompt, own, outs = independent_workers(ours, OracleOps, torch.float32, "cpu")
+    for w in range(2):
+        ref = ref_logits(model, torch.cat([prompt, own[w]]))
+        for i, o in enumerate(outs):
+            assert torch.allclose(o[w, -1], ref[len(prompt) + i], atol=1e-4, rtol=1e-4), (w, i)
+
+
+def test_workers_sharing_a_write_segment_append_in_turn_cpu():
+    """Two workers whose new tokens go to one segment: worker 0's rows first,
+    then worker 1's (attention.py:141-152 appends the workers in turn); no row
+    is overwritten and none is left unwritten."""
+    from dvattention_amd import hf
+    model = surgery_copy(tiny_qwen2(torch.float32, "cpu"))
+    pool = hf.SegmentPool(model.config, 2, 32, torch.float32, "cpu")
+    run_steps(model, hf.DVAttnCache([[pool[0]]], model, ops=OracleOps), [torch.tensor([[1, 2, 3]])])
+    shared = hf.DVAttnCache([[pool[0], pool[1]], [pool[0], pool[1]]], model, write_to=[pool[1], pool[1]],
+                            ops=OracleOps)
+    ids = torch.tensor([[4, 5], [6, 7]])
+    kw = shared.get_input_kwargs(ids)
+    captured = []
+    orig = OracleOps.kv_append
+
+    def spy(keys, values, positions, cos, sin, k_pages, v_pages, block_tables):
+        captured.append((keys.clone(), values.clone(), positions.clone()))
+        orig(keys, values, positions, cos, sin, k_pages, v_pages, block_tables)
+
+    shared.ops = type("SpyOps", (OracleOps,), {"kv_append": staticmethod(spy)})
+    with torch.no_grad():
+        model(**kw)
+    assert [pool[1].get_seq_length(l) for l in range(2)] == [4, 4]
+    keys, values, positions = captured[0]                   # layer 0
+    assert torch.equal(positions, torch.tensor([[0, 1], [2, 3]], dtype=torch.int32))
+    v_seg = pool.v[0][1]                                    # [Hkv, capacity, E]
+    assert torch.equal(v_seg[:, 0:2], values[0])
+    assert torch.equal(v_seg[:, 2:4], values[1])
+    assert torch.all(v_seg[:, 4:] == 0)
+
+
+def test_segments_from_transformers_caches_cpu():
+    """A prompt prefilled by transformers itself (its DynamicCache) copied into a
+    pool segment, then decoded through the DVAttn module: the logits follow
+    transformers' forward on the whole sequence."""
+    from dvattention_amd import hf
+    model = tiny_qwen2(torch.float32, "cpu")
+    ours = surgery_copy(model)
+    g = torch.Generator().manual_seed(8)
+    toks = torch.randint(0, 320, (12,), generator=g)
+    with torch.no_grad():
+        pre = model(input_ids=toks[None, :9], use_cache=True).past_key_values
+    pool = hf.SegmentPool(ours.config, 1, 64, torch.float32, "cpu")
+    segs = hf.segments_from_caches([pre], pool)
+    assert [segs[0].get_seq_length(l) for l in range(2)] == [9, 9]
+    outs = run_steps(ours, hf.DVAttnCache([segs], ours, ops=OracleOps), [toks[9 + i:10 + i][None] for i in range(3)])
+    ref = ref_logits(model, toks)
+    for i, o in enumerate(outs):
+        assert torch.allclose(o[0, -1], ref[9 + i], atol=1e-4, rtol=1e-4), i
+
+
+def test_reference_import_path_cpu():
+    """``import dvattn.attention`` (the reference's module path) registers the
+    operators and exposes the reference's names over this build."""
+    import dvattn.attention as A
+    import dvattention_amd
+    from dvattention_amd import hf
+    assert hasattr(torch.ops.libdvatt, "dvattn_paged_sdpa")
+    for name in ("dvattn_fused", "dvattn_sdpa", "dvattn_sdpa_pt", "dvattn_rope", "rotate_half",
+                 "apply_rotary_pos_emb"):
+        assert getattr(A, name) is getattr(dvattention_amd, name)
+    for name in ("CacheStructure", "DVAttnCache", "merge_caches", "AttentionModule", "model_surgery"):
+        assert getattr(A, name) is getattr(hf, name)
+
+
 # ------------------------------------------------------------------ GPU --
 
 @pytest.mark.gpu
@@ -213,3 +296,48 @@ def test_cross_visible_workers_and_merge_match_oracle_gpu(gpu):
         assert torch.allclose(x, y, atol=5e-4, rtol=1e-4), (x - y).abs().max().item()
     for x, y in zip(ca, cb):
         assert torch.allclose(x, y, atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 5e-4), (torch.bfloat16, 6e-2)])
+def test_eager_and_hip_modules_agree_gpu(gpu, dtype, tol):
+    """The module's PyTorch attention ("eager") and the HIP dvattn_fused path,
+    both on the GPU with the HIP cache operations, on cross-visible workers."""
+    from dvattention_amd import hf
+    base = tiny_qwen2(dtype, gpu, seed=5)
+    g = torch.Generator().manual_seed(6)
+    prompt = torch.randint(0, 320, (9,), generator=g).to(gpu)
+    own = torch.randint(0, 320, (2, 3), generator=g).to(gpu)
+    results = []
+    for attn in ("eager", "sdpa"):
+        model = surgery_copy(base, attn=attn)
+        pool = hf.SegmentPool(model.config, 3, 64, dtype, gpu)
+        run_steps(model, hf.DVAttnCache([[pool[0]]], model, ops=hf.HipOps), [prompt[None]])
+        cache = hf.DVAttnCache([[pool[0], pool[2], pool[1]], [pool[0], pool[1], pool[2]]], model, ops=hf.HipOps)
+        results.append(run_steps(model, cache, [own[:, i:i + 1] for i in range(3)]))
+    for x, y in zip(*results):
+        err = (x - y).abs().max().item()
+        assert err <= tol, err
+
+
+@pytest.mark.gpu
+def test_reference_import_path_gpu(gpu):
+    """``from dvattn.attention import dvattn_fused`` runs the HIP operator
+    (configuration 1's shape) and matches the oracle."""
+    from dvattn.attention import dvattn_fused
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(1, 16, 1, 128, generator=g)
+    k = torch.randn(1, 1, 512, 128, generator=g)
+    v = torch.randn(1, 1, 512, 128, generator=g)
+    loc = torch.tensor([[[512]]], dtype=torch.int32)
+    fl = torch.tensor([512], dtype=torch.int32)
+    ang = 512 * (1e4 ** (-torch.arange(0, 64, 2, dtype=torch.float64) / 64))
+    c = torch.cat([ang, ang]).cos().float().reshape(1, 1, 1, 64)
+    s = torch.cat([ang, ang]).sin().float().reshape(1, 1, 1, 64)
+    rq = torch.empty(1, 1, 16, 1, 128, device=gpu)
+    out = torch.empty(1, 16, 1, 128, device=gpu)
+    dvattn_fused(q.to(gpu), loc.to(gpu), [k.to(gpu)], [v.to(gpu)], 128 ** -0.5, fl.to(gpu), c.to(gpu), s.to(gpu),
+                 rotated_queries=rq, out=out)
+    ref, rq_ref = O.fused(128 ** -0.5, loc, q, fl, [k], [v], c, s)
+    assert torch.equal(rq.cpu(), rq_ref)
+    assert (out.cpu() - ref).abs().max().item() <= 1e-5
