@@ -107,6 +107,63 @@ def time_config(i: int, steps: int, warmup: int, device) -> dict:
     return res
 
 
+def read_ceiling(i: int, steps: int, warmup: int, device) -> dict:
+    """The paged-read probe (dvattention_amd/csrc/dv_probe.hip, libdvattn_probe.so)
+    on configuration i's inputs: the decode kernel's K/V stream -- same work
+    split, launch shape, page-id cache, direct-to-LDS ring and waits -- with the
+    attention taken out.  Timed like time_config (back-to-back calls over the
+    same input replicas, HIP events on the launch stream); the rate is the
+    visible K/V bytes per call over the time."""
+    import ctypes
+    from dvattention_amd import capi
+    from dvattention_amd import workloads as WL
+    lib = ctypes.CDLL(os.path.join(HERE, "dvattention_amd", "libdvattn_probe.so"))
+    lib.dvprobe_last_error.restype = ctypes.c_char_p
+    lib.dvprobe_paged_read.restype = ctypes.c_int
+    lib.dvprobe_paged_read.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 6 + [ctypes.c_void_p, ctypes.c_size_t,
+                                                                                  ctypes.c_void_p, ctypes.c_longlong,
+                                                                                  ctypes.c_void_p]
+    first = WL.config(i, device=device, seed=1234)
+    if first.op != "paged" or first.meta["S"] != 1:
+        raise ValueError(f"config {i}: the read probe covers one-view paged decode configurations")
+    R = replicas_for(first.meta.get("kv_bytes", first.alg_bytes))
+    wls = [first] + [WL.config(i, device=device, seed=1234 + r) for r in range(1, R)]
+    args = []
+    for w in wls:
+        t = w.t
+        shp = capi.paged_shape(t["queries"], t["locations"], t["cosines"], t["k_cache"], t["v_cache"],
+                               t["block_tables"])
+        ws = torch.empty(1 << 20, dtype=torch.uint8, device=device)
+        sink = torch.empty(4 * 4096, dtype=torch.int32, device=device)
+        args.append((shp, ws, sink, t))
+    stream = torch.cuda.current_stream()
+
+    def call(j):
+        shp, ws, sink, t = args[j % R]
+        rc = lib.dvprobe_paged_read(capi.dtype_code(first.dtype), t["locations"].data_ptr(),
+                                    t["fragment_lengths"].data_ptr(), t["k_cache"].data_ptr(),
+                                    t["v_cache"].data_ptr(), t["block_tables"].data_ptr(), ctypes.byref(shp),
+                                    ws.data_ptr(), ws.numel(), sink.data_ptr(), sink.numel(), stream.cuda_stream)
+        if rc != 0:
+            raise RuntimeError(lib.dvprobe_last_error().decode())
+
+    for j in range(warmup):
+        call(j)
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for j in range(steps):
+        call(j)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1e3 / steps
+    kv = sum(w.meta["kv_bytes"] for w in wls) / R
+    del wls, args
+    torch.cuda.empty_cache()
+    return {"config": i, "workload": first.name, "probe_us_per_call": round(us, 2), "kv_bytes": int(kv),
+            "read_GBs": round(kv / (us * 1e-6) / 1e9, 1), "read_frac": round(kv / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
 def _time_calls(fn, n_inputs: int, steps: int, warmup: int) -> tuple:
     """Mean µs per call of fn(j % n_inputs): (a) `steps` eager back-to-back calls
     (HIP events; small kernels are bound by the host's launch rate there) and
@@ -278,6 +335,8 @@ def main() -> int:
     ap.add_argument("--configs", default="1,2,3,4,5")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-cache-rows", action="store_true", help="skip the K-side append / view metadata rows")
+    ap.add_argument("--read-ceiling", action="store_true",
+                    help="only the paged-read probe on configurations 2 and 4 (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the operator has no multi-GPU path); "
@@ -288,6 +347,17 @@ def main() -> int:
         return 2
     import dvattention_amd  # noqa: F401  (loads the HIP libraries; fails loudly if missing)
     device = torch.device("cuda", 0)
+    if args.read_ceiling:
+        rows = []
+        for i in (2, 4):
+            rows.append(read_ceiling(i, args.steps, args.warmup, device))
+            dec = time_config(i, args.steps, args.warmup, device)
+            rows[-1]["decode_us_per_call"] = dec["us_per_call"]
+            rows[-1]["decode_kernel_us"] = dec["kernel_us_mean"]
+            log(f"[bench] read probe cfg{i}: {rows[-1]['probe_us_per_call']} us/call, {rows[-1]['read_GBs']} GB/s "
+                f"(decode {dec['us_per_call']} us/call)")
+        print(json.dumps({"read_ceiling": rows}), flush=True)
+        return 0
     cfgs = [int(x) for x in args.configs.split(",") if x]
     if 2 not in cfgs:
         cfgs = [2] + cfgs
@@ -312,6 +382,9 @@ def main() -> int:
             traffic = json.load(f)
     copy_gbs = measure_copy(device)
     log(f"[bench] device copy (1 GiB read + 1 GiB write): {copy_gbs:.0f} GB/s")
+    ceiling = read_ceiling(2, args.steps, args.warmup, device)
+    log(f"[bench] read probe cfg2 (decode access pattern, no compute): {ceiling['probe_us_per_call']} us/call, "
+        f"{ceiling['read_GBs']} GB/s")
     cpu = None if args.no_cpu else cpu_baseline(device)
     line = {
         "metric": METRIC,
@@ -333,7 +406,8 @@ def main() -> int:
                      "frac": head["hbm_frac"], "traffic": traffic.get("traffic_bytes_per_call"),
                      "traffic_source": traffic.get("source"),
                      "kernel": "dv_stream + dv_merge (one call)", "alg_bytes_per_launch": head["alg_bytes"],
-                     "launch_us": head["kernel_us_mean"], "copy_GBs": round(copy_gbs, 1)},
+                     "launch_us": head["kernel_us_mean"], "copy_GBs": round(copy_gbs, 1),
+                     "read_ceiling": ceiling},
         "cpu_baseline": cpu,
         "per_config": [per[i] for i in sorted(per)],
         "cache_rows": cache_rows,

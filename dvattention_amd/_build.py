@@ -25,6 +25,8 @@ ARCH = os.environ.get("DVATTN_ARCH", "gfx950")
 
 CAPI_SO = os.path.join(HERE, "libdvattn_amd.so")
 TORCH_SO = os.path.join(HERE, "_libdvatt.so")
+# measurement-only library: the paged-read probe behind `bench.py --read-ceiling`
+PROBE_SO = os.path.join(HERE, "libdvattn_probe.so")
 
 HIP_SOURCES = ["dv_decode.hip", "dv_chunk.hip", "dv_rope.hip", "dv_cache.hip", "dv_capi.hip"]
 
@@ -84,9 +86,18 @@ def build_torch_ops() -> str:
     return TORCH_SO
 
 
+def build_probe() -> str:
+    hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
+    tmp = PROBE_SO + ".tmp"
+    _run([hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", os.path.join(CSRC, "dv_probe.hip"), "-o", tmp])
+    os.replace(tmp, PROBE_SO)
+    return PROBE_SO
+
+
 def build_all() -> None:
     build_capi()
     build_torch_ops()
+    build_probe()
 
 
 if __name__ == "__main__":

@@ -11,6 +11,7 @@
 
 #include "../../include/dvattn_amd.h"
 #include "dv_common.h"
+#include "dv_stream.h"
 
 namespace {
 
@@ -174,7 +175,7 @@ dvattn_status dvattn_paged_sdpa(int dtype, void* out, float scale, const int* lo
     p.bs_shift = log2_exact(s->block_size);
     p.maxB = s->max_blocks_per_seq;
     p.nblocks = s->num_blocks;
-    p.min_keys = 64;
+    p.min_keys = dv::kDecodeMinKeys;
     const long long max_keys = (long long)s->max_blocks_per_seq * s->block_size;
     hipError_t e;
     if (dv::use_chunk(dtype, s->S)) {
@@ -265,7 +266,7 @@ dvattn_status dvattn_varlen_paged_sdpa(int dtype, void* out, float scale, const 
     p.bs_shift = log2_exact(s->block_size);
     p.maxB = s->max_blocks_per_seq;
     p.nblocks = s->num_blocks;
-    p.min_keys = 64;
+    p.min_keys = dv::kDecodeMinKeys;
     const long long max_keys = (long long)s->max_blocks_per_seq * s->block_size;
     hipError_t e = dv::launch_decode(dtype, dv::kQRotHalf, dv::kKvPaged, dv::kRowVarlen, p, s->total_q_tokens,
                                      max_keys, workspace, workspace_bytes, (hipStream_t)stream);
@@ -350,7 +351,7 @@ dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* location
     p.R = 0;
     p.bs = 1;
     p.bs_shift = 0;
-    p.min_keys = 64;
+    p.min_keys = dv::kDecodeMinKeys;
     hipError_t e;
     if (dv::use_chunk(dtype, s->S)) {
         p.min_keys = 256;

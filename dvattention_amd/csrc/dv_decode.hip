@@ -28,6 +28,7 @@
 #include "dv_common.h"
 #include "dv_device.h"
 #include "dv_schedule.h"
+#include "dv_stream.h"
 
 namespace dv {
 
@@ -37,117 +38,6 @@ constexpr int kVtBytes16 = kStep * kVtStride16;  // 9216 B per wave
 constexpr int kVtBytes32 = kStep * kVtStride32;  // 16896 B per wave
 
 template <int DT> constexpr int vt_bytes() { return DT == kF32 ? kVtBytes32 : kVtBytes16; }
-
-// ---- row / view helpers -------------------------------------------------------
-
-template <int RM>
-__device__ inline int row_loc(const DecodeParams& p, int row, int f) {
-    if (RM == kRowVarlen) return p.loc[(long long)f * p.T + row];
-    const int w = row / p.S;
-    const int s = row - w * p.S;
-    return p.loc[((long long)f * p.W + w) * p.S + s];
-}
-
-template <int KVM>
-__device__ inline const FragDesc& frag(const DecodeParams& p, int f) {
-    return f < kMaxFragArgs ? p.frags[f] : p.frag_tab[f];
-}
-
-// Visible keys of view f for a query at location locv:
-// min(L_f, loc + 1) clamped at 0 (paged_kernel_v21.cuh:83-85); varlen views with
-// loc < 0 are skipped (varlen_paged_kernel_v21.cuh:76-80), which is the same count.
-template <int KVM>
-__device__ inline int view_vis(const DecodeParams& p, int f, int locv) {
-    long long L = p.fl[f];
-    if (KVM == kKvContig) L = L < frag<KVM>(p, f).L ? L : frag<KVM>(p, f).L;
-    long long v = (long long)locv + 1;
-    v = v < L ? v : L;
-    return v > 0 ? (int)v : 0;
-}
-
-template <int KVM, int RM>
-__device__ inline long long row_visible(const DecodeParams& p, int row) {
-    // views four at a time, their loads issued together (one memory round trip
-    // per four views instead of two per view)
-    long long v = 0;
-    int f = 0;
-    for (; f + 4 <= p.F; f += 4) {
-        int lc[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) lc[j] = row_loc<RM>(p, row, f + j);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v += view_vis<KVM>(p, f + j, lc[j]);
-    }
-    for (; f < p.F; ++f) v += view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
-    return v;
-}
-
-// The views of one query row, view f in lane f (F <= 64), from one round of
-// loads: visible keys, visible keys of the earlier views, and logical position
-// of the view's key 0 (sum of the earlier fragment_lengths).
-struct ViewTab {
-    int vis;
-    long long P, off;
-};
-
-template <int KVM, int RM>
-__device__ inline ViewTab view_table(const DecodeParams& p, int row) {
-    const int lane = threadIdx.x & 63;
-    int vis = 0;
-    long long fl = 0;
-    if (lane < p.F) {
-        vis = view_vis<KVM>(p, lane, row_loc<RM>(p, row, lane));
-        fl = p.fl[lane];
-    }
-    long long sv = vis, so = fl;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const long long tv = __shfl_up(sv, d, kWave);
-        const long long to = __shfl_up(so, d, kWave);
-        if (lane >= d) {
-            sv += tv;
-            so += to;
-        }
-    }
-    return ViewTab{vis, sv - vis, so - fl};
-}
-
-// Calls body(f, vis, P, off) for every view of `row` with visible keys in the
-// row's visible-key range [v0, v1), in view order.
-template <int KVM, int RM, class Body>
-__device__ inline void for_views(const DecodeParams& p, int row, long long v0, long long v1, Body&& body) {
-    if (p.F <= kWave) {
-        const int lane = threadIdx.x & 63;
-        const ViewTab t = view_table<KVM, RM>(p, row);
-        uint64_t m = ballot(lane < p.F && t.vis > 0 && t.P < v1 && t.P + t.vis > v0);
-        while (m) {
-            const int f = __builtin_ctzll(m);
-            m &= m - 1;
-            body(f, __shfl(t.vis, f, kWave), __shfl(t.P, f, kWave), __shfl(t.off, f, kWave));
-        }
-        return;
-    }
-    long long P = 0, off = 0;
-    for (int f = 0; f < p.F && P < v1; ++f) {
-        const int vis = view_vis<KVM>(p, f, row_loc<RM>(p, row, f));
-        if (vis > 0 && P + vis > v0) body(f, vis, P, off);
-        P += vis;
-        off += p.fl[f];
-    }
-}
-
-// Sequence of packed token t: first i with t < cu_seqlens_q[i+1], else 0
-// (varlen_paged_kernel_v21.cuh:40-47).  Wave-cooperative, 64 entries per ballot.
-__device__ inline int varlen_seq(const DecodeParams& p, int t) {
-    const int lane = threadIdx.x & 63;
-    for (int base = 0; base < p.W; base += kWave) {
-        const int i = base + lane;
-        const bool hit = i < p.W && t < p.cu_q[i + 1];
-        const uint64_t b = ballot(hit);
-        if (b) return base + __builtin_ctzll(b);
-    }
-    return 0;
-}
 
 // ---- per-wave K/V staging -----------------------------------------------------
 
@@ -209,22 +99,6 @@ __device__ inline long long kv_row(const DecodeParams& p, const KvCtx& c, const 
     } else {
         const long long off = c.bstride + ((long long)c.hkv * c.L + key) * kHeadDim;
         return key < l1 ? off : -1;
-    }
-}
-
-// Rows of zeros that invisible keys load from, so every lane issues the same
-// loads (no divergent branches around the memory instructions).
-__device__ __align__(16) unsigned char g_zero_row[512];
-
-// Logical page and in-page offset of a logical key position (32-bit, as the
-// reference's absolute_key_pos, paged_kernel_v21.cuh:103-104).
-__device__ inline void page_split(const DecodeParams& p, uint32_t pos, uint32_t& lp, uint32_t& r) {
-    if (p.bs_shift >= 0) {
-        lp = pos >> p.bs_shift;
-        r = pos & ((1u << p.bs_shift) - 1u);
-    } else {
-        lp = pos / (uint32_t)p.bs;
-        r = pos - lp * (uint32_t)p.bs;
     }
 }
 
@@ -516,68 +390,6 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
 // per-wave LDS page cache, so the loop issues no other vector-memory operation.
 
 namespace stream {
-
-constexpr int kTile = kStep * 256;           // one K (or V) stage tile: 32 keys x 256 B
-constexpr int kStage = 2 * kTile;            // K tile then V tile
-constexpr int kRing = 2;                     // stages per wave
-constexpr int kPc = 512;                     // page ids cached per wave
-constexpr int kWaveLds = kRing * kStage + kPc * 4;
-
-struct View {
-    const unsigned char* k;  // paged: the cache; contiguous: K row 0 of (batch entry, head)
-    const unsigned char* v;
-    int off;                 // paged: logical position of the view's key 0
-    int lp0;                 // paged: logical page of page-cache entry 0
-    int b;                   // end (exclusive) of the current view-local key range
-    int hkv;
-};
-
-// Issue the 16 direct-to-LDS loads of the stage holding keys [l, l+32) into the
-// ring slot at LDS address sbase.  Load i moves key rows 4i .. 4i+3: lane ->
-// (row lane/16, swizzled piece).  Returns the visibility mask of the 32 keys.
-template <int KVM>
-__device__ inline uint32_t issue(const DecodeParams& p, const View& v, const int* pc, uint32_t sbase, int l) {
-    const int lane = threadIdx.x & 63;
-    const int c16 = lane & 15, sub = lane >> 4;
-    // addresses of the 8 key rows first (page-cache reads batched), then the loads
-    const unsigned char* ka[8];
-    const unsigned char* va[8];
-    bool ok[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int kk = i * 4 + sub;
-        const int key = l + kk;
-        unsigned long long boff;
-        if (KVM == kKvPaged) {
-            const int pos = v.off + key;
-            uint32_t lp, r;
-            page_split(p, pos > 0 ? (uint32_t)pos : 0u, lp, r);
-            const uint32_t idx = lp - (uint32_t)v.lp0;
-            const bool in = key < v.b && pos >= 0 && idx < (uint32_t)kPc;
-            const int page = in ? pc[in ? idx : 0u] : -1;
-            ok[i] = page >= 0;
-            const uint32_t rowidx = ((uint32_t)page * (uint32_t)p.bs + r) * (uint32_t)p.Hkv + (uint32_t)v.hkv;
-            boff = (unsigned long long)rowidx << 8;
-        } else {
-            ok[i] = key < v.b;
-            boff = (unsigned long long)(uint32_t)key << 8;
-        }
-        const int gk = c16 ^ (kk & 15), gv = c16 ^ ((kk & 7) << 1);
-        ka[i] = ok[i] ? v.k + boff + gk * 16 : g_zero_row + gk * 16;
-        va[i] = ok[i] ? v.v + boff + gv * 16 : g_zero_row + gv * 16;
-    }
-    uint32_t mask = 0;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        dma16(ka[i], sbase + (uint32_t)(i * 1024));
-        dma16(va[i], sbase + (uint32_t)(kTile + i * 1024));
-        const uint64_t bl = ballot(ok[i]);
-        const uint32_t bits = (uint32_t)(bl & 1u) | (uint32_t)((bl >> 15) & 2u) | (uint32_t)((bl >> 30) & 4u) |
-                              (uint32_t)((bl >> 45) & 8u);
-        mask |= bits << (i * 4);
-    }
-    return mask;
-}
 
 // One stage on MFMA: S^T = K Q^T from the K tile, online softmax, O^T += V^T P^T
 // with V^T from the transposing reads of the V tile.
@@ -1032,25 +844,6 @@ hipError_t note_site(hipError_t e, const char* site) {
 }
 
 int device_cus(int device) { return device_cu_count(device); }
-
-int pick_hpw(int Hkv) {
-    if (Hkv % 4 == 0) return 4;
-    if (Hkv % 2 == 0) return 2;
-    return 1;
-}
-
-// Start cost of a piece in the 16-bit decode's work split, in keys: about the
-// time a workgroup needs to restart its pipeline on a new segment.
-constexpr int kPieceCost = 128;
-
-// Per mille of a chunk the work split moves from each odd workgroup (odd XCD)
-// to the even one before it: measured on MI355X, the odd XCD of each pair ends
-// 5-8 % later with equal chunks, and 40-60 per mille gave the shortest calls
-// on configurations 2-4.  DVATTN_XCD_SKEW_PM overrides it (0: equal chunks).
-int xcd_skew_pm() {
-    static const int v = env_per_mille("DVATTN_XCD_SKEW_PM", 50);
-    return v;
-}
 
 // workgroups per CU such that about eight waves share a CU
 int wgs_per_cu(int hpw) { return 8 / hpw; }

@@ -1,0 +1,192 @@
+// Paged-read probe (libdvattn_probe.so, used by `bench.py --read-ceiling`):
+// the 16-bit decode kernel's K/V stream with the attention taken out.  It runs
+// the decode's work split (run_schedule with the same start cost, XCD skew and
+// minimum range), fills the same per-wave page-id cache and streams every
+// visible K/V row of every piece through the same two-stage direct-to-LDS ring
+// (stream::issue) with the same completion waits -- but computes nothing: each
+// stage is consumed by one LDS word per lane.  Its rate is the HBM read rate
+// the decode's access pattern (256-byte rows of randomly placed pages) can
+// reach on the part, the ceiling the decode kernel is measured against.
+//
+// Single-view paged rows only (the configurations whose ceiling is reported).
+#include <string.h>
+
+#include <atomic>
+
+#include "../../include/dvattn_amd.h"
+#include "dv_common.h"
+#include "dv_device.h"
+#include "dv_schedule.h"
+#include "dv_stream.h"
+
+namespace dv {
+namespace {
+
+// One wave: KV head hkv over visible keys [v0, v1) of a one-view row (the
+// decode's stream::piece minus the query, the MFMAs and the epilogue).
+__device__ unsigned read_piece(const DecodeParams& p, unsigned char* wlds, int row, int hkv, long long v0,
+                               long long v1, long long row_keys) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t ring = __builtin_amdgcn_readfirstlane(lds_addr(wlds));
+    int* pc = reinterpret_cast<int*>(wlds + stream::kRing * stream::kStage);
+    const int w = row / p.S;
+    unsigned acc = 0;
+    if (row_keys <= 0 || v1 <= v0) return acc;
+    stream::View v;
+    v.hkv = hkv;
+    v.k = reinterpret_cast<const unsigned char*>(p.kc);
+    v.v = reinterpret_cast<const unsigned char*>(p.vc);
+    v.off = 0;
+    v.lp0 = 0;
+    const int l0 = (int)v0, l1 = (int)(v1 < row_keys ? v1 : row_keys);
+    const long long span = (long long)(stream::kPc - 1) * p.bs;
+    for (int sa = l0; sa < l1;) {
+        const int sb = (long long)l1 - sa > span ? (int)(sa + span) : l1;
+        v.b = sb;
+        uint32_t lpa, lpz, r;
+        page_split(p, (uint32_t)sa, lpa, r);
+        page_split(p, (uint32_t)(sb - 1), lpz, r);
+        v.lp0 = (int)lpa;
+        const int need = (int)(lpz - lpa) + 1;
+        const int* bt = p.bt + (long long)w * p.maxB;
+        for (int i = lane; i < need; i += kWave) {
+            const uint32_t lp = lpa + (uint32_t)i;
+            int pg = lp < (uint32_t)p.maxB ? bt[lp] : -1;
+            if (pg < 0 || pg >= p.nblocks) pg = -1;
+            pc[i] = pg;
+        }
+        const int n_st = (sb - sa + kStep - 1) / kStep;
+        uint32_t m = stream::issue<kKvPaged>(p, v, pc, ring, sa);
+        if (n_st > 1) m ^= stream::issue<kKvPaged>(p, v, pc, ring + stream::kStage, sa + kStep);
+        for (int s = 0; s < n_st; ++s) {
+            if (s + 1 < n_st) wait_vmcnt<16>();
+            else wait_vmcnt<0>();
+            acc += *reinterpret_cast<const unsigned*>(wlds + (s & 1) * stream::kStage + lane * 4) ^ m;
+            if (s + 2 < n_st) {
+                lds_wait();  // the slot's read is complete before it is refilled
+                m = stream::issue<kKvPaged>(p, v, pc, ring + (uint32_t)((s & 1) * stream::kStage),
+                                            sa + (s + 2) * kStep);
+            }
+        }
+        lds_wait();
+        sa = sb;
+    }
+    return acc;
+}
+
+__global__ __launch_bounds__(256) void dv_read_probe(const DecodeParams p, unsigned* sink) {
+    extern __shared__ __align__(16) unsigned char smem[];
+    __shared__ long long s_scan[4];
+    const int wv = threadIdx.x >> 6;
+    const int HPW = p.hpw;
+    long long* s_pref = reinterpret_cast<long long*>(smem + HPW * stream::kWaveLds);
+    unsigned char* wlds = smem + wv * stream::kWaveLds;
+    unsigned acc = 0;
+    run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<kKvPaged, kRowWS>(p, row); },
+                 [&](int row, int hg, long long v0, long long v1, bool, int, long long rk) {
+        if (wv < HPW) acc += read_piece(p, wlds, row, hg * HPW + wv, v0, v1, rk);
+    });
+    if ((threadIdx.x & 63) == 0) sink[blockIdx.x * kMaxWavesPerWg + wv] = acc;
+}
+
+thread_local const char* g_msg = "";
+
+}  // namespace
+}  // namespace dv
+
+extern "C" {
+
+__attribute__((visibility("default"))) const char* dvprobe_last_error(void) { return dv::g_msg; }
+
+// Streams the visible K/V rows of a single-view 16-bit paged call exactly as
+// dvattn_paged_sdpa's decode kernel does (same split and launch shape) without
+// computing attention.  Arguments as dvattn_paged_sdpa (locations [1,W,1],
+// fragment_lengths [1], caches, block_tables, shape); `workspace` holds the
+// split's merge directory (dvattn_paged_sdpa_workspace_size bytes suffice);
+// `sink` receives one word per wave (4 per workgroup, sink_words >= 4 x CUs).
+// Returns 0, or -1 with a message for dvprobe_last_error().
+__attribute__((visibility("default"))) int dvprobe_paged_read(int dtype, const int* locations,
+                                                               const int* fragment_lengths, const void* k_cache,
+                                                               const void* v_cache, const int* block_tables,
+                                                               const dvattn_shape* s, void* workspace,
+                                                               size_t workspace_bytes, unsigned* sink,
+                                                               long long sink_words, void* stream) {
+    using namespace dv;
+    if (!s || (dtype != DVATTN_BF16 && dtype != DVATTN_F16) || s->F != 1 || s->S != 1 || s->E != 128 ||
+        s->Hq != 16 * s->Hkv || s->Hkv <= 0 || s->W <= 0 || s->W > kMaxRows || s->block_size <= 0) {
+        g_msg = "probe: one-view 16-bit paged decode rows only (F = 1, S = 1, W <= 2048, GQA 16, E = 128)";
+        return -1;
+    }
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        g_msg = "probe: hipGetDevice failed";
+        return -1;
+    }
+    DecodeParams p;
+    memset(&p, 0, sizeof(p));
+    p.loc = locations;
+    p.fl = fragment_lengths;
+    p.kc = k_cache;
+    p.vc = v_cache;
+    p.bt = block_tables;
+    p.F = 1;
+    p.W = s->W;
+    p.S = 1;
+    p.Hq = s->Hq;
+    p.Hkv = s->Hkv;
+    p.bs = s->block_size;
+    p.bs_shift = -1;
+    for (int sh = 0; sh < 31; ++sh)
+        if ((1 << sh) == s->block_size) p.bs_shift = sh;
+    p.maxB = s->max_blocks_per_seq;
+    p.nblocks = s->num_blocks;
+    p.hpw = pick_hpw(p.Hkv);
+    p.piece_cost = kPieceCost;
+    p.min_keys = kDecodeMinKeys;
+    p.skew_pm = xcd_skew_pm();
+    p.row_begin = 0;
+    p.nrows = p.W;
+    const int nhg = p.Hkv / p.hpw;
+    if (workspace_bytes < (size_t)p.nrows * nhg * 2 * sizeof(int) || !workspace) {
+        g_msg = "probe: workspace too small for the merge directory";
+        return -1;
+    }
+    p.dir = reinterpret_cast<int*>(workspace);
+    const size_t lds = (size_t)p.hpw * stream::kWaveLds + (size_t)(p.nrows + 1) * sizeof(long long);
+    static std::atomic<unsigned long long> attr_done{0};
+    hipError_t e = once_per_device(attr_done, device, [&] {
+        const size_t max_lds = (size_t)kMaxWavesPerWg * stream::kWaveLds + (size_t)(kMaxRows + 1) * sizeof(long long);
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_read_probe),
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, (int)max_lds);
+    });
+    if (e != hipSuccess) {
+        g_msg = "probe: hipFuncSetAttribute failed";
+        return -1;
+    }
+    int per_cu = 1;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(&dv_read_probe),
+                                                     p.hpw * kWave, lds) != hipSuccess || per_cu < 1)
+        per_cu = 1;
+    // the decode's launch shape: one wave of resident workgroups, bounded by the work
+    const int cus = device_cu_count(device);
+    long long nwg = (long long)cus * per_cu;
+    const long long max_wg = (long long)cus * (8 / p.hpw);
+    if (nwg > max_wg) nwg = max_wg;
+    const long long cap = ((long long)p.nrows * nhg * s->max_blocks_per_seq * s->block_size + p.min_keys - 1) /
+                          p.min_keys;
+    if (nwg > cap) nwg = cap;
+    p.nwg = nwg < 1 ? 1 : (int)nwg;
+    if (sink_words < (long long)p.nwg * kMaxWavesPerWg || !sink) {
+        g_msg = "probe: sink too small (4 words per workgroup)";
+        return -1;
+    }
+    hipLaunchKernelGGL(dv_read_probe, dim3(p.nwg), dim3(p.hpw * kWave), lds, (hipStream_t)stream, p, sink);
+    if (hipGetLastError() != hipSuccess) {
+        g_msg = "probe: launch failed";
+        return -1;
+    }
+    g_msg = "";
+    return 0;
+}
+
+}  // extern "C"

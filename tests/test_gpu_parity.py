@@ -427,8 +427,10 @@ def test_sdpa_fragment_lengths_below_tensor_length(dv, gpu, dtype, S):
     # fragment_lengths[f] < L_f (a preallocated cache that is only partly
     # filled, as the model integration's segments are): view f's keys are the
     # first fragment_lengths[f] rows of each (batch, head) of the [B,Hkv,L_f,E]
-    # tensor -- the tensor's own strides -- so the result equals the same call
-    # on the tensors cut to those rows, and the oracle (contig_sdpa) agrees
+    # tensor -- the tensor's own strides -- so the call and the same call on the
+    # tensors cut to those rows both match the oracle (contig_sdpa).  (They need
+    # not be bit-identical: the grid size follows the tensor lengths, and with it
+    # the split of the keys into pieces and the fp32 merge's rounding.)
     F, W, Hkv = 3, 2, 2
     Ls, fl = [300, 90, 64], [211, 90, 1]
     g = torch.Generator().manual_seed(77 + S)
@@ -441,8 +443,9 @@ def test_sdpa_fragment_lengths_below_tensor_length(dv, gpu, dtype, S):
                          flt.to(gpu))
     cut = dv.dvattn_sdpa(q.to(gpu), loc.to(gpu), [k[:, :, :n].contiguous().to(gpu) for k, n in zip(keys, fl)],
                          [v[:, :, :n].contiguous().to(gpu) for v, n in zip(vals, fl)], 0.1, flt.to(gpu))
-    assert torch.equal(out, cut)
-    close(out, O.contig_sdpa(0.1, loc, q, flt, keys, vals), dtype, "fragment_lengths < L")
+    ref = O.contig_sdpa(0.1, loc, q, flt, keys, vals)
+    close(out, ref, dtype, "fragment_lengths < L")
+    close(cut, ref, dtype, "tensors cut to fragment_lengths")
 
 
 def test_fused_through_c_abi(gpu):
