@@ -51,11 +51,28 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError(f"build step failed ({proc.returncode}): {' '.join(cmd)}")
 
 
+# Per-source code-generation flags.  dv_chunk.hip: each wave keeps 128 fp32
+# accumulators plus 64 query-operand registers live across its stage loop;
+# with the MFMAs in VGPR form the loop runs without register-file copies,
+# where the compiler's default choice moved accumulators between VGPRs and
+# AGPRs around every MFMA.
+SOURCE_FLAGS = {"dv_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=true"]}
+
+
 def build_capi() -> str:
     hipcc = shutil.which("hipcc") or os.path.join(ROCM, "bin", "hipcc")
-    srcs = [os.path.join(CSRC, s) for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    srcs = [s for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    objs = []
+    for src in srcs:
+        obj = os.path.join(objdir, src.replace(".hip", ".o"))
+        flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+        _run([hipcc, *flags, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+              os.path.join(CSRC, src), "-o", obj])
+        objs.append(obj)
     tmp = CAPI_SO + ".tmp"
-    _run([hipcc, *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", *srcs, "-o", tmp])
+    _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
     os.replace(tmp, CAPI_SO)
     return CAPI_SO
 

@@ -6,21 +6,23 @@
 // paged_kernel_v21.cuh:391); here each K/V row is read once per block of 16
 // tokens.
 //
-//  * Workgroup = eight waves (two per SIMD) on one (sequence, 16-token block,
+//  * Workgroup = four waves, one per SIMD, on one (sequence, 16-token block,
 //    KV head) and a contiguous range of its visible keys.  Wave w owns tokens
-//    2w, 2w+1 of the block: two 16-row query tiles (16 heads each).
-//  * K/V pages stream through a 6-stage LDS ring filled by direct-to-LDS loads
+//    4w .. 4w+3: four 16-row query tiles (16 heads each), so a K/V stage read
+//    from LDS feeds 64 query rows.
+//  * K/V pages stream through an 8-stage LDS ring filled by direct-to-LDS loads
 //    (global_load_lds_dwordx4): 32 keys x 256 B of K and of V per stage, one
-//    eighth issued by each wave, completion tracked with vmcnt and a workgroup
-//    barrier.  The loads never pass through VGPRs; four stages ahead of the one
-//    computed are in flight per CU.
+//    quarter issued by each wave, seven stages ahead of the one computed,
+//    completion tracked with vmcnt and one workgroup barrier per stage.
 //  * Per stage and tile: S^T = K Q^T on 16x16x32 MFMA (8 per tile), online
 //    softmax per query row, O^T += V^T P^T (8 MFMA per tile, 16 for fp16: see
-//    p_operands) with V^T read by the transposing LDS read; K/V operands are
-//    read from LDS once per stage and reused by the wave's two tiles.
-//  * Ping-pong: a stage is an MFMA cluster (S of stage i, P V of stage i - 1)
-//    and a softmax cluster, separated by workgroup barriers; the two waves of a
-//    SIMD run one cluster apart, so one's softmax overlaps the other's MFMAs.
+//    p_operands); the K and V^T operands of a stage are read from LDS once per
+//    wave and kept in registers for its four tiles.
+//  * MFMA / VALU overlap inside the wave: the tiles form two groups (A = 0, 1;
+//    B = 2, 3) that run half a stage apart.  Each half-stage issues one group's
+//    MFMAs (S of B and P V of B's previous stage, or P V of A and S of A's next
+//    stage) while the other group's softmax runs on the VALU, so the two use
+//    disjoint registers and the matrix core stays busy during the softmax.
 //  * Rows are causal-masked per token (key l visible iff l <= locations[f,w,s]).
 //  * The balanced split / LSE merge is the decode kernel's (equal key chunks per
 //    workgroup, fp32 partial slots, dv_merge_chunk).
@@ -31,16 +33,17 @@
 namespace dv {
 namespace chunk {
 
-constexpr int kWaves = 8;                     // waves per workgroup
+constexpr int kWaves = 8;                     // waves per workgroup (two per SIMD)
 constexpr int kThreads = kWaves * kWave;
 constexpr int kTiles = 2;                     // 16-head query tiles (tokens) per wave
+constexpr int kHalf = kTiles / 2;             // tiles per MFMA/VALU group
 constexpr int kTokBlk = kWaves * kTiles;      // tokens per row group
-constexpr int kStages = 6;                    // K/V ring depth
+constexpr int kStages = 8;                    // K/V ring depth
 constexpr int kKvBytes = kStep * 256;         // one K (or V) stage tile: 32 keys x 256 B
 constexpr int kStageBytes = 2 * kKvBytes;     // K tile then V tile
 constexpr int kRingBytes = kStages * kStageBytes;
 constexpr int kPageCap = 2048;                // page ids cached in LDS per view sub-range
-constexpr int kAhead = 4;                     // stages in flight ahead of the one computed
+constexpr int kAhead = 7;                     // stages in flight ahead of the one computed
 constexpr int kDmaPerStage = 2;               // per wave: 1 x K + 1 x V (1 KiB = 4 key rows each)
 
 // Start cost of a piece in the work split, in keys (query staging and rotation,
@@ -76,12 +79,12 @@ struct Range {
 // Byte offset of key l's K (= V) row, or -1 when not visible / not addressable.
 // Paged rows are indexed in 32 bits (the C ABI rejects caches of 2^32 rows or
 // more) and positions are 32-bit as in the reference (paged_kernel_v21.cuh:103-104).
-template <int KVM>
+template <int KVM, bool P2>
 __device__ inline long long row_of(const DecodeParams& p, const Range& r, const int* pages, int l) {
     if (KVM == kKvPaged) {
         const uint32_t pos = (uint32_t)(r.off + l);
         uint32_t lp, rr;
-        if (p.bs_shift >= 0) {
+        if (P2) {  // block_size a power of two
             lp = pos >> p.bs_shift;
             rr = pos & ((1u << p.bs_shift) - 1u);
         } else {
@@ -102,18 +105,32 @@ __device__ inline long long row_of(const DecodeParams& p, const Range& r, const 
 
 // Issue this wave's eighth of stage `st` (keys [kb0, kb0+32) of the range): key
 // rows 4*wave .. 4*wave+3 of K and of V, lane -> (row lane/16, 16-byte piece).
-template <int KVM>
+template <int KVM, bool P2>
 __device__ inline void issue_stage(const DecodeParams& p, const Range& r, const int* pages, uint32_t ring,
                                    int st, int kb0) {
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
     const int pos = lane & 15;
     const uint32_t sbase = ring + (uint32_t)(st % kStages) * kStageBytes;
     const int kl = wv * 4 + (lane >> 4);
-    const long long row = row_of<KVM>(p, r, pages, kb0 + kl);
     const int gk = swz_k(kl, pos), gv = swz_v(kl, pos);
-    const unsigned char* ka = row >= 0 ? r.k + row + gk * 16 : zrow + gk * 16;
-    const unsigned char* va = row >= 0 ? r.v + row + gv * 16 : zrow + gv * 16;
     const uint32_t koff = (uint32_t)(wv * 4) * 256;
+    const unsigned char* ka;
+    const unsigned char* va;
+    if (KVM == kKvPaged && P2 && r.pages_ok && kb0 + kStep <= r.b) {
+        // interior stage of a range whose pages are all valid: no visibility
+        // test and no zero rows
+        const uint32_t pos_l = (uint32_t)(r.off + kb0 + kl);
+        const int pg = pages[(pos_l >> p.bs_shift) - r.lp0];
+        const uint32_t rowidx = (((uint32_t)pg << p.bs_shift) + (pos_l & ((1u << p.bs_shift) - 1u))) *
+                                    (uint32_t)p.Hkv + (uint32_t)r.hkv;
+        const unsigned long long boff = (unsigned long long)rowidx << 8;
+        ka = r.k + boff + gk * 16;
+        va = r.v + boff + gv * 16;
+    } else {
+        const long long row = row_of<KVM, P2>(p, r, pages, kb0 + kl);
+        ka = row >= 0 ? r.k + row + gk * 16 : zrow + gk * 16;
+        va = row >= 0 ? r.v + row + gv * 16 : zrow + gv * 16;
+    }
     dma16(ka, __builtin_amdgcn_readfirstlane(sbase + koff));
     dma16(va, __builtin_amdgcn_readfirstlane(sbase + kKvBytes + koff));
 }
@@ -262,41 +279,269 @@ __device__ inline long long group_visible(const DecodeParams& p, int rg) {
     return total;
 }
 
-// O^T += V^T P^T of one stage for both tiles: block lane sl -> key g*4 + sl/4
-// (+16), dims cc*16 + (sl%4)*4; row k0 (and k0 + 16), piece (cc*2 + b) ^
-// ((k0 & 7) << 1), byte hb: the swizzle only flips address bits 5-7 of vbase, so
-// slice cc is at vbase ^ (32 cc).  Each 16-dim slice of V^T is read once for both
-// tiles; all sixteen reads are issued before the first MFMA.
-template <int DT>
-__device__ inline void pv_stage(const unsigned char* vt, const POperand (&pB)[kTiles], Tile (&tl)[kTiles]) {
+// K operand of one stage (A of S^T = K Q^T): lo[cc] holds key n, hi[cc] key
+// 16 + n, dims cc*32 + g*8 .. +8 (lane (g, n)).  The K swizzle only flips
+// address bits 6-7 of the row base, so slice cc is at kbase ^ (64 cc).
+struct KOp {
+    u32x4 lo[4], hi[4];
+};
+
+// V^T operand of one stage (A of O^T += V^T P^T), 16-dim slice cc: block lane
+// sl -> key g*4 + sl/4 (and + 16), dims cc*16 + (sl%4)*4 (transposing reads);
+// the V swizzle only flips address bits 5-7, so slice cc is at vbase ^ (32 cc).
+struct VOp {
+    u32x4 v[8];
+};
+
+__device__ inline void read_k(const unsigned char* kt, KOp& k) {
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    const uint32_t kbase = lds_addr(kt) + (uint32_t)(n * 256 + 16 * (g ^ (n & 3)) + 64 * (n >> 2));
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        k.lo[cc] = lds_read16_at(kbase ^ (uint32_t)(64 * cc));
+        k.hi[cc] = lds_read16_at((kbase ^ (uint32_t)(64 * cc)) + 16 * 256);
+    }
+}
+
+__device__ inline void read_v(const unsigned char* vt, VOp& v) {
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, sl = lane & 15;
     const int k0 = g * 4 + (sl >> 2);
     const uint32_t vbase =
         lds_addr(vt) + (uint32_t)(k0 * 256 + 16 * ((sl & 3) >> 1) + (sl & 1) * 8 + 32 * (k0 & 7));
-    u32x4 va[8];
 #pragma unroll
     for (int cc = 0; cc < 8; ++cc) {
         const u32x2 a0 = lds_read_tr16_at(vbase ^ (uint32_t)(32 * cc));
         const u32x2 a1 = lds_read_tr16_at((vbase ^ (uint32_t)(32 * cc)) + 16 * 256);
-        va[cc] = u32x4{a0[0], a0[1], a1[0], a1[1]};
+        v.v[cc] = u32x4{a0[0], a0[1], a1[0], a1[1]};
     }
-    __builtin_amdgcn_sched_barrier(0);
+}
+
+// Scores of one tile: s0 keys 0-15, s1 keys 16-31 (S^T, lane (g, n): keys
+// g*4 + i of head n).
+template <int DT>
+__device__ inline void qk_tile(const KOp& k, const u32x4 (&q)[4], f32x4& s0, f32x4& s1) {
+    s0 = f32x4{0.f, 0.f, 0.f, 0.f};
+    s1 = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int cc = 0; cc < 8; ++cc)
+    for (int cc = 0; cc < 4; ++cc) {
+        s0 = Tr<DT>::mma(k.lo[cc], q[cc], s0);
+        s1 = Tr<DT>::mma(k.hi[cc], q[cc], s1);
+    }
+}
+
+// O^T += V^T P^T for one tile.
+template <int DT>
+__device__ inline void pv_tile(const VOp& v, const POperand& pB, Tile& t) {
 #pragma unroll
-        for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va[cc], pB[t].hi, tl[t].o[cc]);
-    if constexpr (DT == kF16)
+    for (int cc = 0; cc < 8; ++cc) t.o[cc] = Tr<DT>::mma(v.v[cc], pB.hi, t.o[cc]);
+    if constexpr (DT == kF16) {
 #pragma unroll
-        for (int cc = 0; cc < 8; ++cc)
+        for (int cc = 0; cc < 8; ++cc) t.o[cc] = Tr<DT>::mma(v.v[cc], pB.lo, t.o[cc]);
+    }
+}
+
+// Visibility of the 32 keys of the stage starting at kb0: the range end, and,
+// when some page of the sub-range is missing, page validity (a scalar branch
+// around a few instructions; the loop itself is not duplicated).
+template <int KVM, bool P2>
+__device__ inline uint32_t stage_mask(const DecodeParams& p, const Range& r, const int* pages, int sbnd, int kb0) {
+    const int nin = sbnd - kb0;
+    uint32_t m = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
+    if (!r.pages_ok) {
+        const int lane = threadIdx.x & 63;
+        const bool kv_ok = row_of<KVM, P2>(p, r, pages, kb0 + (lane & 31)) >= 0;
+        m &= (uint32_t)ballot(kv_ok && lane < 32);
+    }
+    return m;
+}
+
+// Scores of invisible keys set to -inf (mask bit k = key k; lane (g, n) holds
+// keys g*4 + i and 16 + g*4 + i): a partially visible stage only, so full
+// stages spend nothing on masks.
+__device__ inline void mask_scores(f32x4& s0, f32x4& s1, uint32_t mask) {
+    const int lane = threadIdx.x & 63;
+    const uint32_t mg = mask >> ((lane >> 4) * 4);
 #pragma unroll
-            for (int t = 0; t < kTiles; ++t) tl[t].o[cc] = Tr<DT>::mma(va[cc], pB[t].lo, tl[t].o[cc]);
+    for (int i = 0; i < 4; ++i) {
+        s0[i] = ((mg >> i) & 1u) ? s0[i] : -DV_INF;
+        s1[i] = ((mg >> (16 + i)) & 1u) ? s1[i] : -DV_INF;
+    }
+}
+
+__device__ inline uint32_t token_mask(int vis, int kb0) {
+    const int lim = vis - kb0;
+    return lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
+}
+
+// Online softmax of two tiles over one 32-key stage, in two straight-line
+// parts so that the MFMAs of the other tile group can be interleaved with it
+// (a branch ends the scheduling region).  Scores of invisible keys are -inf
+// already (mask_scores).  Part 1: base-2 exponents against the running max
+// (lane (g, n) holds keys g*4 + i and 16 + g*4 + i of head n); returns the
+// lane's largest, so the caller can ask whether some row exceeds its max by
+// more than kMaxSlack or has no max yet -- then sm_raise (rare) raises the max
+// to the rows' maximum, rescales the accumulators and recomputes the
+// exponents.  Part 2 (sm_finish): the probabilities, the row sums and the P^T
+// operands.  Same arithmetic as softmax32 + p_operands.
+__device__ inline float sm_exponents(const Tile& t, const f32x4& s0, const f32x4& s1, float l2, float (&pr)[8]) {
+    // a row with no max yet (m = -inf) subtracts -FLT_MAX instead: a visible
+    // key's exponent is then huge (the row takes sm_raise) and an invisible
+    // key's stays -inf, where -inf - (-inf) would be NaN
+    const float nm = -fmaxf(t.m, -3.402823466e38f);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        pr[i] = __builtin_fmaf(s0[i], l2, nm);
+        pr[4 + i] = __builtin_fmaf(s1[i], l2, nm);
+    }
+    return fmaxf(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])), fmaxf(fmaxf(pr[4], pr[5]), fmaxf(pr[6], pr[7])));
+}
+
+__device__ inline void sm_raise(Tile& t, const f32x4& s0, const f32x4& s1, float l2, float (&pr)[8]) {
+    float sc[8];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        sc[i] = s0[i] * l2;
+        sc[4 + i] = s1[i] * l2;
+    }
+    const float mx = rows4_max(
+        fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7]))));
+    if (ballot(mx > t.m + kMaxSlack)) {
+        const float mnew = fmaxf(t.m, mx);
+        const float alpha = mnew == -DV_INF ? 1.0f : __builtin_amdgcn_exp2f(t.m - mnew);
+        t.l *= alpha;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) t.o[c] *= alpha;
+        t.m = mnew;
+    }
+    const float mm = t.m == -DV_INF ? 0.0f : t.m;  // p = 0 while the row has no visible key
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pr[i] = sc[i] - mm;
+}
+
+template <int DT>
+__device__ inline POperand sm_finish(Tile& t, float (&pr)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) pr[i] = __builtin_amdgcn_exp2f(pr[i]);
+    return p_operands<DT>(pr, t.l);
+}
+
+// Register tie: the values are complete at this point in program order (the
+// compiler may not move their computation past it, e.g. across a workgroup
+// barrier into the next half-stage).
+__device__ inline void settle(POperand& a) { asm volatile("" : "+v"(a.hi), "+v"(a.lo)); }
+
+// Keys [sa, sbnd) of the current view for this wave's two tiles (A = tile 0,
+// B = tile 1): the stage loop.  Ring slot i % kStages holds stage i.  Per
+// stage i, in every wave:
+//   H1(i): MFMA O_B += V(i-1) P_B(i-1) beside A's exponents; MFMA S_B(i) =
+//          K(i) Q_B^T and read V(i) beside A's probabilities
+//   own loads of stage i+1 landed; workgroup barrier
+//   H2(i): read K(i+1); MFMA O_A += V(i) P_A(i) beside B's exponents; MFMA
+//          S_A(i+1) = K(i+1) Q_A^T and the loads of stage i+kAhead beside B's
+//          probabilities
+// so each wave's instruction stream alternates MFMAs of one tile with the
+// softmax of the other, and the two waves of a SIMD issue both at once.  A
+// slot is refilled (stage i+kAhead into the slot of stage i-1) only after the
+// barrier of stage i+1, which every wave reaches having completed its reads of
+// every stage <= i (the V reads of H1 are waited for before the barrier).  One
+// K and one V^T operand set live in registers: K(i+1) is read after the MFMAs
+// of K(i) are issued, V(i) after those of V(i-1).  A's accumulators are
+// rescaled in H1 and written by MFMAs issued in H2 (and B's the other way
+// round), so a softmax never touches registers an MFMA of the same half-stage
+// writes; mfma_settle before each softmax covers the MFMA -> VALU dependence
+// across the half-stage boundary.  Invisible keys get -inf scores only on a
+// partially visible stage (a uniform branch between the interleaved regions).
+template <int DT, int KVM, bool P2>
+__device__ inline void stream_range(const DecodeParams& p, const Range& r, const int* pages, unsigned char* smem,
+                                    int sa, int sbnd, const int (&vis_t)[kTiles], const u32x4 (&qB)[kTiles][4],
+                                    Tile (&tl)[kTiles]) {
+    const uint32_t ring = lds_addr(smem);
+    const int nsteps = (sbnd - sa + kStep - 1) / kStep;
+    const float l2 = p.l2scale;
+    // prologue: stages 0 .. kAhead-1 (past the end: rows of zeros)
+#pragma unroll
+    for (int st = 0; st < kAhead; ++st) issue_stage<KVM, P2>(p, r, pages, ring, st, sa + st * kStep);
+    wait_vmcnt<kDmaPerStage * (kAhead - 1)>();  // own share of stage 0 landed
+    wg_barrier();
+
+    KOp kop;
+    VOp vop;
+#pragma unroll
+    for (int cc = 0; cc < 8; ++cc) vop.v[cc] = u32x4{0u, 0u, 0u, 0u};  // the first P V adds 0 * 0
+    f32x4 sa0, sa1, sb0, sb1;
+    POperand pa = {}, pb = {};
+    read_k(smem, kop);
+    qk_tile<DT>(kop, qB[0], sa0, sa1);
+
+    for (int i = 0; i < nsteps; ++i) {
+        const int kb0 = sa + i * kStep;
+        const unsigned char* slot = smem + (i % kStages) * kStageBytes;
+        const uint32_t okm = stage_mask<KVM, P2>(p, r, pages, sbnd, kb0);
+        const uint32_t mka = okm & token_mask(vis_t[0], kb0), mkb = okm & token_mask(vis_t[1], kb0);
+        float pr[8];
+        // ---- H1(i)
+        if (mka != 0xffffffffu) mask_scores(sa0, sa1, mka);
+        mfma_settle(tl[0].o);
+        pv_tile<DT>(vop, pb, tl[1]);  // zero at i = 0
+        float lmx = sm_exponents(tl[0], sa0, sa1, l2, pr);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
+        if (ballot(lmx > kMaxSlack)) sm_raise(tl[0], sa0, sa1, l2, pr);
+        qk_tile<DT>(kop, qB[1], sb0, sb1);
+        read_v(slot + kKvBytes, vop);
+        pa = sm_finish<DT>(tl[0], pr);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
+        settle(pa);
+        lds_wait();
+        wait_vmcnt<kDmaPerStage * (kAhead - 2)>();  // own share of stage i + 1 landed
+        wg_barrier();
+        // ---- H2(i) (stage i + 1 has landed even past the end -- rows of zeros --
+        // so K and S_A of the next stage need no branch; the last ones go unused)
+        read_k(smem + ((i + 1) % kStages) * kStageBytes, kop);
+        if (mkb != 0xffffffffu) mask_scores(sb0, sb1, mkb);
+        mfma_settle(tl[1].o);
+        pv_tile<DT>(vop, pa, tl[0]);
+        lmx = sm_exponents(tl[1], sb0, sb1, l2, pr);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // LDS read
+            __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+        }
+        if (ballot(lmx > kMaxSlack)) sm_raise(tl[1], sb0, sb1, l2, pr);
+        qk_tile<DT>(kop, qB[0], sa0, sa1);
+        pb = sm_finish<DT>(tl[1], pr);
+        // the loads of stage i + kAhead (into the slot of stage i - 1, free since
+        // the barrier), their address arithmetic beside the MFMAs
+        issue_stage<KVM, P2>(p, r, pages, ring, i + kAhead, sa + (i + kAhead) * kStep);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
+        }
+        settle(pb);
+    }
+    // P V of B's last stage
+    mfma_settle(tl[1].o);
+    pv_tile<DT>(vop, pb, tl[1]);
 #pragma unroll
     for (int t = 0; t < kTiles; ++t) mfma_settle(tl[t].o);
+    wait_vmcnt<0>();  // the trailing zero-row stages land before the ring is reused
+    __syncthreads();
 }
 
 // One workgroup: keys [v0, v1) of row group rg for KV head hkv.
-template <int DT, int QM, int KVM>
+template <int DT, int QM, int KVM, bool P2>
 __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pages, int rg, int hkv, long long v0,
                             long long v1, bool final_out, int slot) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
@@ -305,7 +550,6 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
     const int w = rg / nsb, sb = rg - (rg / nsb) * nsb;
     const int tok0 = sb * kTokBlk + wv * kTiles;      // this wave's first token
     const int ntile = p.S - tok0 < kTiles ? (p.S - tok0 > 0 ? p.S - tok0 : 0) : kTiles;
-    const uint32_t ring = lds_addr(smem);
 
     Tile tl[kTiles];
 #pragma unroll
@@ -381,86 +625,7 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                     }
                     r.pages_ok = __syncthreads_and(ok) != 0;
                 }
-                const int nsteps = (sbnd - sa + kStep - 1) / kStep;
-                // Ping-pong: the stage loop alternates an MFMA cluster X_i (S = K Q^T of
-                // stage i, O += V P of stage i - 1) and a VALU cluster Y_i (softmax of
-                // stage i, then the loads of stage i + kAhead), with a workgroup barrier
-                // between clusters.  Waves 4-7 start one cluster behind waves 0-3 (wave
-                // w runs on SIMD w % 4), so the two waves of each SIMD run X and Y at
-                // the same time.  Every wave passes 2 * nsteps + 1 barriers.  Ring slot
-                // (i + kAhead) % kStages held stage i - 2, whose V was last read in
-                // X_{i-1}, finished by both groups before either starts Y_i.
-                // uniform in the wave (a scalar branch: the group's extra barrier must
-                // not execute with an empty exec mask in the other group's waves)
-                const int grp = __builtin_amdgcn_readfirstlane(wv >> 2);
-                const unsigned char* vt_prev = smem;  // V tile of the previous stage
-                POperand pB[kTiles] = {};              // its P^T operands
-                // prologue: stages 0 .. kAhead-1 (past the end: rows of zeros)
-#pragma unroll
-                for (int st = 0; st < kAhead; ++st) issue_stage<KVM>(p, r, pages, ring, st, sa + st * kStep);
-                wait_vmcnt<kDmaPerStage * (kAhead - 1)>();  // own share of stage 0 landed
-                if (grp) wg_barrier();
-                for (int i = 0; i < nsteps; ++i) {
-                    wg_barrier();  // stage i landed for every wave
-                    // ---- X_i
-                    const int kb0 = sa + i * kStep;
-                    const unsigned char* kt = smem + (i % kStages) * kStageBytes;
-                    // S^T = K Q^T for both tiles: the K operand of each 32-dim slice is
-                    // read once and used by both (tiles past the token count have a zero
-                    // query and no visible key, so they need no branch)
-                    f32x4 s0[kTiles], s1[kTiles];
-#pragma unroll
-                    for (int t = 0; t < kTiles; ++t) {
-                        s0[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-                        s1[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-                    }
-                    // K row n (and 16 + n), piece (cc*4 + g) ^ n: the swizzle only flips
-                    // address bits 6-7 of kbase, so slice cc is at kbase ^ (64 cc).  All
-                    // eight operand reads are issued before the first MFMA, so their LDS
-                    // latency overlaps the MFMAs instead of preceding each pair.
-                    const uint32_t kbase = lds_addr(kt) + (uint32_t)(n * 256 + 16 * (g ^ (n & 3)) + 64 * (n >> 2));
-                    u32x4 ka[4], kb[4];
-#pragma unroll
-                    for (int cc = 0; cc < 4; ++cc) {
-                        ka[cc] = lds_read16_at(kbase ^ (uint32_t)(64 * cc));
-                        kb[cc] = lds_read16_at((kbase ^ (uint32_t)(64 * cc)) + 16 * 256);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                    for (int cc = 0; cc < 4; ++cc) {
-#pragma unroll
-                        for (int t = 0; t < kTiles; ++t) {
-                            s0[t] = Tr<DT>::mma(ka[cc], qB[t][cc], s0[t]);
-                            s1[t] = Tr<DT>::mma(kb[cc], qB[t][cc], s1[t]);
-                        }
-                    }
-                    if (i > 0) pv_stage<DT>(vt_prev, pB, tl);
-                    vt_prev = kt + kKvBytes;
-                    __builtin_amdgcn_sched_barrier(0);
-                    wait_vmcnt<kDmaPerStage * (kAhead - 2)>();  // own share of stage i + 1 landed
-                    wg_barrier();
-                    // ---- Y_i: visibility of the 32 keys (the range end, and page validity
-                    // when some page of the sub-range is missing), then the softmax
-                    uint32_t okmask;
-                    if (r.pages_ok) {
-                        const int nin = sbnd - kb0;
-                        okmask = nin >= 32 ? 0xffffffffu : ((1u << nin) - 1u);
-                    } else {
-                        const bool kv_ok = row_of<KVM>(p, r, pages, kb0 + (lane & 31)) >= 0;
-                        okmask = (uint32_t)ballot(kv_ok && lane < 32);
-                    }
-#pragma unroll
-                    for (int t = 0; t < kTiles; ++t) {
-                        const int lim = vis_t[t] - kb0;
-                        const uint32_t lm = lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
-                        pB[t] = tile_softmax<DT>(tl[t], s0[t], s1[t], okmask & lm, p.l2scale);
-                    }
-                    issue_stage<KVM>(p, r, pages, ring, i + kAhead, sa + (i + kAhead) * kStep);
-                }
-                if (!grp) wg_barrier();
-                if (nsteps > 0) pv_stage<DT>(vt_prev, pB, tl);
-                wait_vmcnt<0>();    // the trailing zero-row stages land before the ring is reused
-                __syncthreads();
+                stream_range<DT, KVM, P2>(p, r, pages, smem, sa, sbnd, vis_t, qB, tl);
             }
         }
         P += vis_blk;
@@ -499,7 +664,9 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
     }
 }
 
-template <int DT, int QM, int KVM>
+// P2: paged with a power-of-two block_size (shift and mask instead of a
+// division in the stage loop's row addressing).
+template <int DT, int QM, int KVM, bool P2>
 __global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     // the ring starts at a 256-byte aligned LDS address (the XOR addressing of
@@ -512,7 +679,7 @@ __global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
 
     run_schedule(p, NHG, s_pref, s_scan, [&](int rg) { return group_visible<KVM>(p, rg); },
                  [&](int rg, int hg, long long v0, long long v1, bool fin, int slot, long long) {
-                     chunk_piece<DT, QM, KVM>(p, smem, pages, rg, hg, v0, v1, fin, slot);
+                     chunk_piece<DT, QM, KVM, P2>(p, smem, pages, rg, hg, v0, v1, fin, slot);
                  });
 }
 
@@ -585,11 +752,11 @@ size_t lds_bytes(int nrows) {
     return 256 + (size_t)kRingBytes + (size_t)kPageCap * 4 + (size_t)(kWaves + nrows + 1) * sizeof(long long);
 }
 
-template <int DT, int QM, int KVM>
-hipError_t launch(DecodeParams p, int device, int cus, long long cap, hipStream_t stream) {
+template <int DT, int QM, int KVM, bool P2>
+hipError_t launch1(DecodeParams p, int device, int cus, long long cap, hipStream_t stream) {
     static std::atomic<unsigned long long> attr_done{0};
     hipError_t ea = once_per_device(attr_done, device, [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_chunk<DT, QM, KVM>),
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_chunk<DT, QM, KVM, P2>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes(kMaxRows));
     });
     if (ea != hipSuccess) return ea;
@@ -597,11 +764,18 @@ hipError_t launch(DecodeParams p, int device, int cus, long long cap, hipStream_
     long long nwg = cus;  // one eight-wave workgroup per CU (LDS ring 96 KiB)
     if (nwg > cap) nwg = cap;
     p.nwg = nwg < 1 ? 1 : (int)nwg;
-    hipLaunchKernelGGL((dv_chunk<DT, QM, KVM>), dim3(p.nwg), dim3(kThreads), lds, stream, p);
+    hipLaunchKernelGGL((dv_chunk<DT, QM, KVM, P2>), dim3(p.nwg), dim3(kThreads), lds, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     hipLaunchKernelGGL((dv_merge_chunk<DT>), dim3(p.nrows * p.Hkv * kTokBlk), dim3(256), 0, stream, p);
     return hipGetLastError();
+}
+
+template <int DT, int QM, int KVM>
+hipError_t launch(DecodeParams p, int device, int cus, long long cap, hipStream_t stream) {
+    if constexpr (KVM == kKvPaged)
+        if (p.bs_shift >= 0) return launch1<DT, QM, KVM, true>(p, device, cus, cap, stream);
+    return launch1<DT, QM, KVM, false>(p, device, cus, cap, stream);
 }
 
 }  // namespace chunk

@@ -55,7 +55,8 @@ def close(gpu_out, ref, dtype, what=""):
     g, r = gpu_out.float().cpu(), ref.float()
     err = (g - r).abs()
     tol = TOL[dtype]
-    miss = err > tol
+    miss = ~(err <= tol)  # NaN counts as a miss
+    assert not torch.isnan(r).any(), f"{what}: NaN in the reference"
     forgiven = 0
     if miss.any() and dtype in MANT:
         rr = r.to(dtype).float()

@@ -25,11 +25,13 @@ from test_gpu_parity import close
     (torch.float16, 5.0, 5.00390625, False),          # one ulp in [4,8) > 1e-3 + half ulp
     (torch.float16, 5.001, 5.00390625, True),         # 2.91e-3 <= 2.95e-3
     (torch.float32, 1.0, 1.0 + 2e-5, False),
+    (torch.float32, 1.0, float("nan"), False),       # NaN never passes
+    (torch.bfloat16, 9.0, float("nan"), False),
     (torch.float32, 1.0, 1.0 + 5e-6, True),
 ])
 def test_rule(dtype, ref, out, ok):
     g = torch.tensor([out], dtype=torch.float32).to(dtype)
-    if dtype != torch.float32:
+    if dtype != torch.float32 and out == out:
         assert g.float().item() == out
     r = torch.tensor([ref], dtype=torch.float32)
     if ok:
