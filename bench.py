@@ -376,10 +376,10 @@ def main() -> int:
     # HBM bytes per call from the committed rocprofv3 --pmc summary (FETCH_SIZE / WRITE_SIZE
     # scaled by a 1 GiB copy); absent -> null
     traffic = {}
-    tpath = os.path.join(HERE, "profiles", "dv_stream_cfg2_hbm_traffic.json")
+    tpath = os.path.join(HERE, "profiles", "hbm_traffic_configs2-5.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f)
+            traffic = next((t for t in json.load(f) if t.get("config") == head["config"]), {})
     copy_gbs = measure_copy(device)
     log(f"[bench] device copy (1 GiB read + 1 GiB write): {copy_gbs:.0f} GB/s")
     ceiling = read_ceiling(2, args.steps, args.warmup, device)
