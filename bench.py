@@ -44,8 +44,10 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def replicas_for(wl_bytes: int, max_replicas: int = 8) -> int:
-    # enough distinct inputs that the rotation's footprint is >= 4x the Infinity Cache
+def replicas_for(wl_bytes: int, max_replicas: int = 4096) -> int:
+    # enough distinct inputs that the rotation's footprint is >= 4x the Infinity
+    # Cache, so every call reads its K/V from HBM (configuration 1's 0.5 MB
+    # takes about 1900 replicas)
     need = max(1, -(-4 * MALL_BYTES // max(1, wl_bytes)))
     return min(max_replicas, need)
 

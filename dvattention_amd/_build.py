@@ -11,6 +11,7 @@ Both libraries land next to this file so they travel with the source tree.
 """
 from __future__ import annotations
 
+import concurrent.futures
 import os
 import shutil
 import subprocess
@@ -28,7 +29,7 @@ TORCH_SO = os.path.join(HERE, "_libdvatt.so")
 # measurement-only library: the paged-read probe behind `bench.py --read-ceiling`
 PROBE_SO = os.path.join(HERE, "libdvattn_probe.so")
 
-HIP_SOURCES = ["dv_decode.hip", "dv_chunk.hip", "dv_rope.hip", "dv_cache.hip", "dv_capi.hip"]
+HIP_SOURCES = ["dv_decode.hip", "dv_chunk.hip", "dv_small.hip", "dv_rope.hip", "dv_cache.hip", "dv_capi.hip"]
 
 # gfx950 code only; packed-fp32 instructions are disabled (the host pass of
 # hipcc warns that it does not know the feature, which is harmless).
@@ -64,13 +65,15 @@ def build_capi() -> str:
     srcs = [s for s in HIP_SOURCES if os.path.exists(os.path.join(CSRC, s))]
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = []
-    for src in srcs:
-        obj = os.path.join(objdir, src.replace(".hip", ".o"))
-        flags = [f for f in HIPCC_FLAGS if f != "-shared"]
-        _run([hipcc, *flags, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
-              os.path.join(CSRC, src), "-o", obj])
-        objs.append(obj)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+    objs = [os.path.join(objdir, src.replace(".hip", ".o")) for src in srcs]
+    cmds = [[hipcc, *flags, *SOURCE_FLAGS.get(src, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c",
+             os.path.join(CSRC, src), "-o", obj] for src, obj in zip(srcs, objs)]
+    # one compiler per source, a few at a time (each takes about 1 GB)
+    workers = max(1, min(len(cmds), 4, os.cpu_count() or 1))
+    with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
+        for fut in [pool.submit(_run, c) for c in cmds]:
+            fut.result()
     tmp = CAPI_SO + ".tmp"
     _run([hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp])
     os.replace(tmp, CAPI_SO)

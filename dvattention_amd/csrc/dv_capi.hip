@@ -283,15 +283,23 @@ size_t dvattn_sdpa_workspace_size(int dtype, const dvattn_shape* s, int device) 
            contig_table_bytes(s->F);
 }
 
-dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* locations, const void* rotated_queries,
-                          const int* fragment_lengths, const void* const* key_fragments,
-                          const void* const* value_fragments, const int* fragment_tokens,
-                          const int* fragment_batch, const dvattn_shape* s, void* workspace,
-                          size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// dvattn_sdpa's argument checks (binding.cu:79-149, plus the shapes the
+// reference ignored) and its launch parameters: p, the view table and the
+// longest row's key count.  `empty`: nothing to compute.
+dvattn_status sdpa_setup(int dtype, void* out, float scale, const int* locations, const void* rotated_queries,
+                         const int* fragment_lengths, const void* const* key_fragments,
+                         const void* const* value_fragments, const int* fragment_tokens, const int* fragment_batch,
+                         const dvattn_shape* s, void* workspace, size_t workspace_bytes, dv::DecodeParams& p,
+                         std::vector<dv::FragDesc>& tab, long long& max_keys, bool& empty) {
+    empty = true;
     if (!s) return fail(DVATTN_ERR_INVALID, "shape is null");
     if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
     if (s->F < 0 || s->W < 0 || s->S < 0) return fail(DVATTN_ERR_INVALID, "negative F/W/S");
-    if ((long long)s->W * s->S == 0 || s->Hkv == 0) return ok();
+    if ((long long)s->W * s->S == 0 || s->Hkv == 0) return DVATTN_OK;
     dvattn_status st;
     if ((st = check_heads(s)) != DVATTN_OK) return st;
     if (!out || !rotated_queries) return fail(DVATTN_ERR_INVALID, "null output or query pointer");
@@ -302,12 +310,9 @@ dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* location
     if (workspace_bytes < need || (need && !workspace))
         return fail(DVATTN_ERR_WORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
 
-    dv::DecodeParams p;
     memset(&p, 0, sizeof(p));
-    const size_t tab_bytes = contig_table_bytes(s->F);
-    std::vector<dv::FragDesc> tab((size_t)s->F);
-    long long max_keys = 0;
-    const size_t esz = dtype == DVATTN_F32 ? 4 : 2;
+    tab.assign((size_t)s->F, dv::FragDesc{});
+    max_keys = 0;
     for (int f = 0; f < s->F; ++f) {
         const int L = fragment_tokens[f];
         const int B = fragment_batch[f];
@@ -327,17 +332,6 @@ dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* location
         max_keys += L;
         if (f < dv::kMaxFragArgs) p.frags[f] = d;
     }
-    (void)esz;
-    void* ws = workspace;
-    size_t ws_left = workspace_bytes;
-    if (tab_bytes) {
-        hipError_t e = hipMemcpyAsync(workspace, tab.data(), (size_t)s->F * sizeof(dv::FragDesc),
-                                      hipMemcpyHostToDevice, (hipStream_t)stream);
-        if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa fragment table upload");
-        p.frag_tab = reinterpret_cast<const dv::FragDesc*>(workspace);
-        ws = reinterpret_cast<unsigned char*>(workspace) + tab_bytes;
-        ws_left -= tab_bytes;
-    }
     p.out = out;
     p.loc = locations;
     p.q = rotated_queries;
@@ -352,42 +346,99 @@ dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* location
     p.bs = 1;
     p.bs_shift = 0;
     p.min_keys = dv::kDecodeMinKeys;
+    empty = false;
+    return DVATTN_OK;
+}
+
+// The general contiguous-view launch: view table (F > kMaxFragArgs) to the
+// workspace, then the decode or chunk kernel on already-rotated queries.
+dvattn_status sdpa_launch(int dtype, dv::DecodeParams& p, const std::vector<dv::FragDesc>& tab, long long max_keys,
+                          void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    void* ws = workspace;
+    size_t ws_left = workspace_bytes;
+    const size_t tab_bytes = contig_table_bytes(p.F);
+    if (tab_bytes) {
+        hipError_t e =
+            hipMemcpyAsync(workspace, tab.data(), (size_t)p.F * sizeof(dv::FragDesc), hipMemcpyHostToDevice, stream);
+        if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa fragment table upload");
+        p.frag_tab = reinterpret_cast<const dv::FragDesc*>(workspace);
+        ws = reinterpret_cast<unsigned char*>(workspace) + tab_bytes;
+        ws_left -= tab_bytes;
+    }
     hipError_t e;
-    if (dv::use_chunk(dtype, s->S)) {
+    if (dv::use_chunk(dtype, p.S)) {
         p.min_keys = 256;
-        e = dv::launch_chunk(dtype, dv::kQPre, dv::kKvContig, p, max_keys, ws, ws_left, (hipStream_t)stream);
+        e = dv::launch_chunk(dtype, dv::kQPre, dv::kKvContig, p, max_keys, ws, ws_left, stream);
     } else {
-        e = dv::launch_decode(dtype, dv::kQPre, dv::kKvContig, dv::kRowWS, p, s->W * s->S, max_keys, ws, ws_left,
-                              (hipStream_t)stream);
+        e = dv::launch_decode(dtype, dv::kQPre, dv::kKvContig, dv::kRowWS, p, p.W * p.S, max_keys, ws, ws_left,
+                              stream);
     }
     if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa launch");
     return ok();
 }
 
-dvattn_status dvattn_fused(int dtype, void* out, void* rotated_queries, float scale, const int* locations,
-                           const void* queries, const int* fragment_lengths, const void* const* key_fragments,
-                           const void* const* value_fragments, const int* fragment_tokens,
-                           const int* fragment_batch, const float* cosines, const float* sines,
-                           const dvattn_shape* s, void* workspace, size_t workspace_bytes, void* stream) {
-    dvattn_status st = dvattn_rope(dtype, rotated_queries, queries, cosines, sines, s, stream);
-    if (st != DVATTN_OK) return st;
-    return dvattn_sdpa(dtype, out, scale, locations, rotated_queries, fragment_lengths, key_fragments,
-                       value_fragments, fragment_tokens, fragment_batch, s, workspace, workspace_bytes, stream);
+// Whether the single-launch path takes a validated contiguous-view call: fp32,
+// at most kMaxFragArgs views of at most kSmallMaxChunks chunks together, and
+// its partials within the documented workspace size of the shape (so the
+// choice depends on the shape and the fragment lengths only); rotating calls
+// (dvattn_fused) also need rotary_dim % 8 == 0.  Returns the chunk count, or -1
+// for the general path.
+// DVATTN_SMALL_PATH (read on every call): "0" turns the path off; "require"
+// makes a call it cannot take fail with DVATTN_ERR_UNSUPPORTED (*refused).
+int small_path_chunks(int dtype, const dvattn_shape* s, const int* fragment_tokens, bool rotating, bool* refused) {
+    *refused = false;
+    const char* env = getenv("DVATTN_SMALL_PATH");
+    if (env && env[0] == '0') return -1;
+    const bool require = env && strcmp(env, "require") == 0;
+    int chunks = -1;
+    if (dtype == DVATTN_F32 && s->F >= 1 && s->F <= dv::kMaxFragArgs && (!rotating || s->rotary_dim % 8 == 0)) {
+        chunks = dv::small_chunks(s->F, fragment_tokens);
+        const long long items = (long long)s->W * s->S * s->Hkv;
+        if (chunks >= 1 && dv::small_workspace_bytes(items, chunks) > dvattn_sdpa_workspace_size(dtype, s, -1))
+            chunks = -1;
+    }
+    if (chunks < 1 && require) {
+        fail(DVATTN_ERR_UNSUPPORTED,
+             "DVATTN_SMALL_PATH=require: the single-launch path takes fp32 calls of 1-%d views with at most %d "
+             "chunks of %d keys per row (and rotary_dim %% 8 == 0 when it rotates)",
+             dv::kMaxFragArgs, dv::kSmallMaxChunks, dv::kSmallChunk);
+        *refused = true;
+    }
+    return chunks;
 }
 
-// ---------------------------------------------------------------------------
-dvattn_status dvattn_rope(int dtype, void* out, const void* queries, const float* cosines, const float* sines,
-                          const dvattn_shape* s, void* stream) {
+dvattn_status small_launch(int dtype, int qmode, const dv::DecodeParams& p, int chunks, const int* fragment_tokens,
+                           void* rq_out, void* workspace, hipStream_t stream) {
+    dv::SmallParams sp;
+    memset(&sp, 0, sizeof(sp));
+    sp.d = p;
+    sp.rq = rq_out;
+    sp.chunks = chunks;
+    int c = 0;
+    for (int f = 0; f < p.F; ++f) {
+        sp.first_chunk[f] = c;
+        const int L = fragment_tokens[f];
+        c += L > 0 ? (L + dv::kSmallChunk - 1) / dv::kSmallChunk : 1;
+    }
+    sp.first_chunk[p.F] = c;
+    const hipError_t e = dv::launch_small(dtype, qmode, sp, workspace, stream);
+    if (e != hipSuccess) return hip_fail(e, "single-launch attention");
+    return ok();
+}
+
+// dvattn_rope's checks (rope.cuh:54-65) into p; `empty`: nothing to rotate.
+dvattn_status rope_setup(int dtype, void* out, const void* queries, const float* cosines, const float* sines,
+                         const dvattn_shape* s, dv::RopeParams& p, bool& empty) {
+    empty = true;
     if (!s) return fail(DVATTN_ERR_INVALID, "shape is null");
     if (!valid_dtype(dtype)) return fail(DVATTN_ERR_UNSUPPORTED, "unsupported dtype code %d", dtype);
     if (s->F < 0 || s->W < 0 || s->Hq < 0 || s->S < 0 || s->E < 0)
         return fail(DVATTN_ERR_INVALID, "negative size");
     dvattn_status st;
     if ((st = check_rotary(s->rotary_dim, s->E)) != DVATTN_OK) return st;
-    if ((long long)s->F * s->W * s->Hq * s->S * s->E == 0) return ok();  // rope.cuh:58-60
+    if ((long long)s->F * s->W * s->Hq * s->S * s->E == 0) return DVATTN_OK;  // rope.cuh:58-60
     if (!out || !queries || (s->rotary_dim > 0 && (!cosines || !sines)))
         return fail(DVATTN_ERR_INVALID, "null pointer");
-    dv::RopeParams p;
     memset(&p, 0, sizeof(p));
     p.out = out;
     p.q = queries;
@@ -400,6 +451,82 @@ dvattn_status dvattn_rope(int dtype, void* out, const void* queries, const float
     p.E = s->E;
     p.R = s->rotary_dim;
     p.half_width = 0;
+    empty = false;
+    return DVATTN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+dvattn_status dvattn_sdpa(int dtype, void* out, float scale, const int* locations, const void* rotated_queries,
+                          const int* fragment_lengths, const void* const* key_fragments,
+                          const void* const* value_fragments, const int* fragment_tokens,
+                          const int* fragment_batch, const dvattn_shape* s, void* workspace,
+                          size_t workspace_bytes, void* stream) {
+    dv::DecodeParams p;
+    std::vector<dv::FragDesc> tab;
+    long long max_keys = 0;
+    bool empty = true;
+    dvattn_status st = sdpa_setup(dtype, out, scale, locations, rotated_queries, fragment_lengths, key_fragments,
+                                  value_fragments, fragment_tokens, fragment_batch, s, workspace, workspace_bytes, p,
+                                  tab, max_keys, empty);
+    if (st != DVATTN_OK) return st;
+    if (empty) return ok();
+    bool refused = false;
+    const int chunks = small_path_chunks(dtype, s, fragment_tokens, false, &refused);
+    if (refused) return DVATTN_ERR_UNSUPPORTED;
+    if (chunks > 0)
+        return small_launch(dtype, dv::kQPre, p, chunks, fragment_tokens, nullptr, workspace, (hipStream_t)stream);
+    return sdpa_launch(dtype, p, tab, max_keys, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// binding.cu:356-372: rotate the queries into rotated_queries, attend on them.
+// Both steps' arguments are checked before anything runs; short views take the
+// single launch that rotates, attends and merges.
+dvattn_status dvattn_fused(int dtype, void* out, void* rotated_queries, float scale, const int* locations,
+                           const void* queries, const int* fragment_lengths, const void* const* key_fragments,
+                           const void* const* value_fragments, const int* fragment_tokens,
+                           const int* fragment_batch, const float* cosines, const float* sines,
+                           const dvattn_shape* s, void* workspace, size_t workspace_bytes, void* stream) {
+    dv::RopeParams rp;
+    bool no_rope = true;
+    dvattn_status st = rope_setup(dtype, rotated_queries, queries, cosines, sines, s, rp, no_rope);
+    if (st != DVATTN_OK) return st;
+    dv::DecodeParams p;
+    std::vector<dv::FragDesc> tab;
+    long long max_keys = 0;
+    bool empty = true;
+    st = sdpa_setup(dtype, out, scale, locations, rotated_queries, fragment_lengths, key_fragments, value_fragments,
+                    fragment_tokens, fragment_batch, s, workspace, workspace_bytes, p, tab, max_keys, empty);
+    if (st != DVATTN_OK) return st;
+    bool refused = false;
+    const int chunks = empty || no_rope ? -1 : small_path_chunks(dtype, s, fragment_tokens, true, &refused);
+    if (refused) return DVATTN_ERR_UNSUPPORTED;
+    if (chunks > 0) {
+        p.q = queries;
+        p.cosv = cosines;
+        p.sinv = sines;
+        p.R = s->rotary_dim;
+        return small_launch(dtype, dv::kQRotFull, p, chunks, fragment_tokens, rotated_queries, workspace,
+                            (hipStream_t)stream);
+    }
+    if (!no_rope) {
+        const hipError_t e = dv::launch_rope(dtype, rp, (hipStream_t)stream);
+        if (e != hipSuccess) return hip_fail(e, "dvattn_rope launch");
+    }
+    if (empty) return ok();
+    return sdpa_launch(dtype, p, tab, max_keys, workspace, workspace_bytes, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+dvattn_status dvattn_rope(int dtype, void* out, const void* queries, const float* cosines, const float* sines,
+                          const dvattn_shape* s, void* stream) {
+    dv::RopeParams p;
+    bool empty = true;
+    const dvattn_status st = rope_setup(dtype, out, queries, cosines, sines, s, p, empty);
+    if (st != DVATTN_OK) return st;
+    if (empty) return ok();
     hipError_t e = dv::launch_rope(dtype, p, (hipStream_t)stream);
     if (e != hipSuccess) return hip_fail(e, "dvattn_rope launch");
     return ok();

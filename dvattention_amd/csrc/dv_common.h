@@ -78,6 +78,24 @@ struct DecodeParams {
     FragDesc frags[kMaxFragArgs];
 };
 
+// Single-launch path for short contiguous views (dv_small.hip): one workgroup
+// per (query row, KV head, chunk of kSmallChunk tensor keys of one view).  The
+// query rotation (dvattn_fused), the attention and the merge of the chunks all
+// run in that one launch; the last workgroup of a (row, KV head) to finish
+// merges its chunks.  Rotating mode needs rotary_dim % 8 == 0.
+constexpr int kSmallChunk = 64;       // tensor keys per workgroup (16 per wave)
+constexpr int kSmallMaxChunks = 64;   // chunks per (row, KV head): up to 4096 keys
+
+struct SmallParams {
+    DecodeParams d;                   // out, loc, q, cosv, sinv, fl, frags, l2scale, F, W, S, Hq, Hkv, R
+    void* rq;                         // rotated queries [F,W,Hq,S,E] written here (rotating mode), or null
+    float* part;                      // [items][chunks][kGqa * (kHeadDim + 1)]: normalised output, base-2 LSE
+    unsigned long long* flags;        // [items][chunks] arrival flags (raised: == tag)
+    unsigned long long tag;           // this call's flag value (48 bits, nonzero)
+    int chunks;                       // chunks per item (row, KV head)
+    int first_chunk[kMaxFragArgs + 1];  // first chunk of view f; first_chunk[F] = chunks
+};
+
 struct RopeParams {
     void* out;
     const void* q;
@@ -167,6 +185,13 @@ inline bool use_chunk(int dtype, int S) { return S >= 2 && dtype != kF32; }
 size_t chunk_workspace_bytes(int W, int S, int Hkv, int device);
 hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& base, long long max_keys_per_group,
                         void* workspace, size_t ws_bytes, hipStream_t stream);
+// Single-launch path (fp32 contiguous views): chunks per item for F views of
+// fragment_tokens toks, or -1 when the views are too many or too long; the
+// workspace it needs for `items` (row, KV head) items; the launch (qmode kQPre
+// or kQRotFull).  launch_small fills p.part / p.flags / p.tag from the workspace.
+int small_chunks(int F, const int* toks);
+size_t small_workspace_bytes(long long items, int chunks);
+hipError_t launch_small(int dtype, int qmode, SmallParams& p, void* workspace, hipStream_t stream);
 // Which runtime call produced the last error returned by launch_decode (this thread).
 const char* last_hip_site();
 

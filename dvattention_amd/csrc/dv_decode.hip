@@ -175,84 +175,6 @@ __device__ inline void compute32(SoftState& st, const Kv32& b, const f32x4 (&qB)
     compiler_fence();
 }
 
-// ---- query operand ------------------------------------------------------------
-
-// 16-bit: lane (g, n) holds Q[n][c*32 + g*8 + 0..7] for c = 0..3 (B operand of S^T).
-template <int DT, int QM, int RM>
-__device__ inline void load_q16(const DecodeParams& p, int row, int f, int hkv, u32x4 (&qB)[4]) {
-    using raw = typename Tr<DT>::raw;
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, n = lane & 15;
-    const int h = hkv * kGqa + n;
-    if (QM == kQPre) {
-        const int w = row / p.S, s = row - (row / p.S) * p.S;
-        const raw* q = reinterpret_cast<const raw*>(p.q) +
-                       ((((long long)f * p.W + w) * p.Hq + h) * p.S + s) * kHeadDim;
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) qB[cc] = ld16(q + cc * 32 + g * 8);
-        return;
-    }
-    const raw* q;
-    const float* cs;
-    const float* sn;
-    if (QM == kQRotFull) {
-        const int w = row / p.S, s = row - (row / p.S) * p.S;
-        q = reinterpret_cast<const raw*>(p.q) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
-        const long long co = (((long long)f * p.W + w) * p.S + s) * p.R;
-        cs = p.cosv + co;
-        sn = p.sinv + co;
-    } else {
-        q = reinterpret_cast<const raw*>(p.q) + ((long long)row * p.Hq + h) * kHeadDim;
-        const long long co = ((long long)f * p.T + row) * (p.R >> 1);
-        cs = p.cosv + co;
-        sn = p.sinv + co;
-    }
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-        raw r[8];
-        rotate_run<DT, 8>(q, cs, sn, p.R, cc * 32 + g * 8, r);
-        qB[cc] = u32x4{(uint32_t)r[0] | ((uint32_t)r[1] << 16), (uint32_t)r[2] | ((uint32_t)r[3] << 16),
-                       (uint32_t)r[4] | ((uint32_t)r[5] << 16), (uint32_t)r[6] | ((uint32_t)r[7] << 16)};
-    }
-}
-
-// fp32: lane (g, n) holds Q[n][c*16 + g*4 + 0..3] for c = 0..7.
-template <int QM, int RM>
-__device__ inline void load_q32(const DecodeParams& p, int row, int f, int hkv, f32x4 (&qB)[8]) {
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, n = lane & 15;
-    const int h = hkv * kGqa + n;
-    if (QM == kQPre) {
-        const int w = row / p.S, s = row - (row / p.S) * p.S;
-        const float* q = reinterpret_cast<const float*>(p.q) +
-                         ((((long long)f * p.W + w) * p.Hq + h) * p.S + s) * kHeadDim;
-#pragma unroll
-        for (int cc = 0; cc < 8; ++cc) qB[cc] = ld16f(q + cc * 16 + g * 4);
-        return;
-    }
-    const float* q;
-    const float* cs;
-    const float* sn;
-    if (QM == kQRotFull) {
-        const int w = row / p.S, s = row - (row / p.S) * p.S;
-        q = reinterpret_cast<const float*>(p.q) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
-        const long long co = (((long long)f * p.W + w) * p.S + s) * p.R;
-        cs = p.cosv + co;
-        sn = p.sinv + co;
-    } else {
-        q = reinterpret_cast<const float*>(p.q) + ((long long)row * p.Hq + h) * kHeadDim;
-        const long long co = ((long long)f * p.T + row) * (p.R >> 1);
-        cs = p.cosv + co;
-        sn = p.sinv + co;
-    }
-#pragma unroll
-    for (int cc = 0; cc < 8; ++cc) {
-        float r[4];
-        rotate_run<kF32, 4>(q, cs, sn, p.R, cc * 16 + g * 4, r);
-        qB[cc] = f32x4{r[0], r[1], r[2], r[3]};
-    }
-}
-
 // ---- one wave: one KV head over visible keys [v0, v1) of one row ---------------
 
 template <int DT, int QM, int KVM, int RM>

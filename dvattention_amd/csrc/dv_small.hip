@@ -1,0 +1,387 @@
+// Single-launch attention for short contiguous views (ops dvattn_sdpa and
+// dvattn_fused, fp32): the query rotation, the attention and the merge of the
+// key chunks in one kernel, where the general path (dv_decode.hip) takes a
+// rotation launch, a decode launch whose every workgroup first computes the
+// whole work split, and a merge launch.  Same operator semantics as
+// src/kernels/kernel_v21.cuh:17-414 and src/binding.cu:356-372 (reference
+// repository): rotated query per view, softmax over the visible keys of all
+// views, zeros for a query with no visible key.
+//
+//  * Work: the tensor keys of every view are cut into chunks of kSmallChunk; a
+//    workgroup takes one chunk of one (query row, KV head) item, its four waves
+//    16 keys each.  The chunk boundaries depend only on the fragment tensor
+//    lengths (host-known), so every K/V address is known at launch: a
+//    workgroup issues its K/V, query, cos/sin and location loads together and
+//    masks the keys past the view's visible count afterwards.
+//  * A wave computes S^T = K Q^T for its 16 keys x 16 query heads on the fp32
+//    MFMA (16x16x4, dims as the reduction index), the softmax of each head over
+//    its keys, and O = P V with V read straight from global memory (a lane
+//    loads 4 consecutive dims, so output column n of the t-th MFMA is dim
+//    64 b + 4 n + t).  The four waves are combined in LDS.
+//  * Merge: a workgroup stores its chunk's normalised output and base-2
+//    log-sum-exp, then raises its arrival flag and reads the flags of all the
+//    item's chunks; a workgroup that finds them all raised merges every chunk
+//    of the item and writes the output.  A flag is raised by writing the
+//    call's tag, a per-call 48-bit value, so flags need no clearing before a
+//    call (a word left by an earlier call, or arbitrary workspace bytes, hold
+//    another value); a merging workgroup lowers the item's flags to zero, so
+//    the same tag replayed (a captured graph) starts from lowered flags too.
+#include <string.h>
+
+#include <atomic>
+
+#include "dv_common.h"
+#include "dv_device.h"
+#include "dv_stream.h"
+
+namespace dv {
+namespace small {
+
+constexpr int kWaves = 4;
+constexpr int kKeysPerWave = kSmallChunk / kWaves;  // 16: one MFMA key block
+constexpr int kSlot = kGqa * (kHeadDim + 1);         // floats per partial: 16 x 128 outputs, 16 LSE
+constexpr int kMergeBatch = 8;                       // partials loaded together by the merge
+static_assert(kKeysPerWave == 16, "one 16-key MFMA block per wave");
+
+struct Smem {
+    float q[kGqa][kHeadDim];          // the item's query rows (unrotated in rotating mode)
+    float cs[kHeadDim], sn[kHeadDim]; // cos / sin row (rotating mode)
+    float spare[4];                   // written by threads without a cos/sin part (store_query)
+    float o[kWaves][kGqa][kHeadDim];  // each wave's unnormalised output
+    float m[kWaves][kGqa];            // its per-head max (base-2 scores)
+    float l[kWaves][kGqa];            // its per-head sum of exp2(score - max)
+    int last;
+};
+
+// Query rows of the item, staged in LDS: thread t loads dims (t%16)*8 .. +7
+// of head t/16 (rotated queries [F,W,Hq,S,E] in kQPre mode, queries
+// [W,Hq,S,E] otherwise), and in rotating mode threads 0..R/4-1 the cos row,
+// threads 64..64+R/4-1 the sin row of (view, sequence, token).  Loaded into
+// registers first (load_query), stored to LDS after the K/V loads have been
+// issued (store_query), so every global load of the workgroup is in flight
+// at once.
+struct QStage {
+    f32x4 a, b, c;
+    bool trig;
+};
+
+template <int QM>
+__device__ inline QStage load_query(const DecodeParams& p, int w, int s, int f, int hkv) {
+    const int tid = threadIdx.x;
+    const int hh = tid >> 4, dd = (tid & 15) * 8;
+    const long long qrow = QM == kQPre ? ((((long long)f * p.W + w) * p.Hq + hkv * kGqa + hh) * p.S + s) * kHeadDim
+                                       : (((long long)w * p.Hq + hkv * kGqa + hh) * p.S + s) * kHeadDim;
+    const float* q = reinterpret_cast<const float*>(p.q) + qrow + dd;
+    QStage r;
+    r.a = ld16f(q);
+    r.b = ld16f(q + 4);
+    const int j = tid & 63;
+    r.trig = QM != kQPre && tid < 128 && j * 4 < p.R;
+    // a select of the address rather than a branch around the load, so the
+    // waits of the loads after it stay partial
+    const long long co = (((long long)f * p.W + w) * p.S + s) * p.R + j * 4;
+    // both row pointers read as scalars first (a lane-dependent choice between
+    // two kernel arguments is otherwise read with a vector load, one more round trip)
+    const float* cp = p.cosv;
+    const float* sp = p.sinv;
+    asm volatile("" : "+s"(cp), "+s"(sp));
+    r.c = ld16f(r.trig ? (tid < 64 ? cp : sp) + co : reinterpret_cast<const float*>(g_zero_row));
+    return r;
+}
+
+__device__ inline void store_query(const QStage& r, float (*qs)[kHeadDim], float* cs, float* sn, float* spare) {
+    const int tid = threadIdx.x;
+    const int hh = tid >> 4, dd = (tid & 15) * 8;
+    *reinterpret_cast<f32x4*>(&qs[hh][dd]) = r.a;
+    *reinterpret_cast<f32x4*>(&qs[hh][dd + 4]) = r.b;
+    // unconditional store (threads without a cos/sin part write the spare
+    // slot): a conditional one lets the compiler sink the load into the branch
+    float* dst = r.trig ? (tid < 64 ? cs : sn) + (tid & 63) * 4 : spare;
+    *reinterpret_cast<f32x4*>(dst) = r.c;
+}
+
+// Query operand from the staged rows: lane (g, n) holds Q[n][c*16 + g*4 + 0..3],
+// c = 0..7 (the B operand of S^T).  Rotating mode applies the reference's rope
+// (src/rope.cuh:18-51) with the same roundings as rotate_run: separate fp32
+// products, then their difference or sum; dims >= R are copied.  Needs
+// rotary_dim % 8 == 0, so a run of 4 dims never straddles the two halves.
+template <int QM>
+__device__ inline void query_operand(const DecodeParams& p, const float (*qs)[kHeadDim], const float* cs,
+                                     const float* sn, f32x4 (&qB)[8]) {
+#pragma clang fp contract(off)
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    const int half = p.R >> 1;
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+        const int d = c * 16 + g * 4;
+        const f32x4 x = *reinterpret_cast<const f32x4*>(&qs[n][d]);
+        if constexpr (QM == kQPre) {
+            qB[c] = x;
+        } else {
+            const bool rot = d < p.R;
+            const bool first = d < half;
+            const int pd = rot ? (first ? d + half : d - half) : d;
+            const int ci = rot ? (first ? d : pd) : 0;
+            const f32x4 xp = *reinterpret_cast<const f32x4*>(&qs[n][pd]);
+            const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + ci);
+            const f32x4 sv = *reinterpret_cast<const f32x4*>(sn + ci);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float a = x[e] * cv[e];
+                const float b = xp[e] * sv[e];
+                const float y = first ? a - b : a + b;
+                qB[c][e] = rot ? y : x[e];
+            }
+        }
+    }
+}
+
+template <int DT>
+__device__ inline void store8(void* dst, const float (&o)[8], float inv) {
+    if constexpr (DT == kF32) {
+        float* d = reinterpret_cast<float*>(dst);
+        *reinterpret_cast<f32x4*>(d) = f32x4{o[0] * inv, o[1] * inv, o[2] * inv, o[3] * inv};
+        *reinterpret_cast<f32x4*>(d + 4) = f32x4{o[4] * inv, o[5] * inv, o[6] * inv, o[7] * inv};
+    } else {
+        *reinterpret_cast<u32x4*>(dst) = u32x4{pack2<DT>(o[0] * inv, o[1] * inv), pack2<DT>(o[2] * inv, o[3] * inv),
+                                               pack2<DT>(o[4] * inv, o[5] * inv), pack2<DT>(o[6] * inv, o[7] * inv)};
+    }
+}
+
+template <int QM>
+__global__ __launch_bounds__(256) void dv_small32(const SmallParams sp) {
+    __shared__ __align__(16) Smem sm;
+    const DecodeParams& p = sp.d;
+    const int item = blockIdx.x / sp.chunks;  // (query row, KV head)
+    const int ci = blockIdx.x - item * sp.chunks;
+    const int row = item / p.Hkv;
+    const int hkv = item - row * p.Hkv;
+    const int w = row / p.S;
+    const int s = row - w * p.S;
+    int f = 0;
+    while (f + 1 < p.F && sp.first_chunk[f + 1] <= ci) ++f;
+    const FragDesc& fd = p.frags[f];
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int k0 = (ci - sp.first_chunk[f]) * kSmallChunk + wv * kKeysPerWave;  // wave's first tensor key
+    const float* kbase = reinterpret_cast<const float*>(fd.k) + fd.bstride * w + (long long)hkv * fd.L * kHeadDim;
+    const float* vbase = reinterpret_cast<const float*>(fd.v) + fd.bstride * w + (long long)hkv * fd.L * kHeadDim;
+    const float* zrow = reinterpret_cast<const float*>(g_zero_row);
+    const int vis = view_vis<kKvContig>(p, f, row_loc<kRowWS>(p, row, f));
+
+    // ---- loads, all issued together: the query rows and cos/sin (staged in
+    // LDS), K (key k0 + n, dims c*16 + g*4 + 0..3) and V (key k0 + g*4 + i,
+    // dims 64 b + 4 n + 0..3) to registers; keys past the tensor read the zero row
+    const QStage qst = load_query<QM>(p, w, s, f, hkv);
+    f32x4 kr[8], vr[4][2];
+    {
+        const int key = k0 + n;
+        const float* kp = (key < fd.L ? kbase + (long long)key * kHeadDim : zrow) + g * 4;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) kr[c] = ld16f(kp + c * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int key = k0 + g * 4 + i;
+        const float* vp = (key < fd.L ? vbase + (long long)key * kHeadDim : zrow) + n * 4;
+        vr[i][0] = ld16f(vp);
+        vr[i][1] = ld16f(vp + 64);
+    }
+    store_query(qst, sm.q, sm.cs, sm.sn, sm.spare);
+    __syncthreads();
+    f32x4 qB[8];
+    query_operand<QM>(p, sm.q, sm.cs, sm.sn, qB);
+    if (QM == kQRotFull && wv == 0 && ci == sp.first_chunk[f]) {
+        // the view's rotated query, as dvattn_rope writes it
+        float* rq = reinterpret_cast<float*>(sp.rq) +
+                    ((((long long)f * p.W + w) * p.Hq + hkv * kGqa + n) * p.S + s) * kHeadDim + g * 4;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(rq + c * 16) = qB[c];
+    }
+
+    // ---- S^T: lane (g, n) holds keys k0 + g*4 + i of head n
+    f32x4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 8; ++c)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) sc = Tr<kF32>::mma1(kr[c][j], qB[c][j], sc);
+    float pr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = k0 + g * 4 + i < vis ? sc[i] * p.l2scale : -DV_INF;
+    const float mx = rows4_max(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])));
+    const float mm = mx == -DV_INF ? 0.0f : mx;  // p = 0 for a head with no visible key here
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pr[i] = __builtin_amdgcn_exp2f(pr[i] - mm);
+    const float l = rows4_sum((pr[0] + pr[1]) + (pr[2] + pr[3]));
+
+    // ---- O = P V: A = P (head n, key g*4 + i), B = V (key g*4 + i, dim 64 b + 4 n + t);
+    // lane (g, n) receives O[head g*4 + j][dim 64 b + 4 n + t]
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[b][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+            for (int t = 0; t < 4; ++t) acc[b][t] = Tr<kF32>::mma1(pr[i], vr[i][b][t], acc[b][t]);
+    mfma_settle(reinterpret_cast<f32x4(&)[8]>(acc));
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            *reinterpret_cast<f32x4*>(&sm.o[wv][g * 4 + j][b * 64 + n * 4]) =
+                f32x4{acc[b][0][j], acc[b][1][j], acc[b][2][j], acc[b][3][j]};
+    if (g == 0) {
+        sm.m[wv][n] = mx;
+        sm.l[wv][n] = l;
+    }
+    __syncthreads();
+
+    // ---- the chunk: thread (h, d0) combines the four waves for head h, dims d0..d0+7
+    const int h = tid >> 4;
+    const int d0 = (tid & 15) * 8;
+    float M = -DV_INF;
+#pragma unroll
+    for (int k = 0; k < kWaves; ++k) M = fmaxf(M, sm.m[k][h]);
+    float L = 0.0f, o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+    if (M != -DV_INF) {
+#pragma unroll
+        for (int k = 0; k < kWaves; ++k) {
+            const float e = __builtin_amdgcn_exp2f(sm.m[k][h] - M);  // wave without visible keys: 0
+            L += e * sm.l[k][h];
+            const f32x4 a = *reinterpret_cast<const f32x4*>(&sm.o[k][h][d0]);
+            const f32x4 c = *reinterpret_cast<const f32x4*>(&sm.o[k][h][d0 + 4]);
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                o[q] += e * a[q];
+                o[4 + q] += e * c[q];
+            }
+        }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    float* outp = reinterpret_cast<float*>(p.out) + (((long long)w * p.Hq + hkv * kGqa + h) * p.S + s) * kHeadDim + d0;
+    if (sp.chunks == 1) {
+        store8<kF32>(outp, o, inv);
+        return;
+    }
+    float* slot = sp.part + ((long long)item * sp.chunks + ci) * kSlot;
+    store8<kF32>(slot + h * kHeadDim + d0, o, inv);
+    if ((tid & 15) == 0) slot[kGqa * kHeadDim + h] = L > 0.0f ? M + log2f(L) : -DV_INF;
+    // every thread's partial stores complete before the barrier; the agent-scope
+    // release of wave 0 then writes the workgroup's partial back from this XCD's
+    // L2, and the flag is raised after it.  The sequentially consistent fence
+    // between raising the own flag and reading all flags (all in wave 0's
+    // program order) makes the workgroup whose fence comes last see every flag
+    // raised, so at least one workgroup merges; several may, writing the same
+    // output.
+    unsigned long long* flags = sp.flags + (long long)item * sp.chunks;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __syncthreads();
+    if (wv == 0) {
+        if (lane == 0) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+            __hip_atomic_store(flags + ci, sp.tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "agent");
+        const unsigned long long v =
+            lane < sp.chunks ? __hip_atomic_load(flags + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : sp.tag;
+        const bool all = ballot(v != sp.tag) == 0;
+        if (lane == 0) sm.last = all;
+    }
+    __syncthreads();
+    if (!sm.last) return;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // lower the flags (all were raised: no workgroup of this call raises one later)
+    if (tid < sp.chunks) __hip_atomic_store(flags + tid, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+
+    // ---- last arrival: merge the item's chunks (head h, dims d0..d0+7)
+    const float* pbase = sp.part + (long long)item * sp.chunks * kSlot;
+    float m = -DV_INF, wsum = 0.0f, acc8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc8[e] = 0.0f;
+    for (int c0 = 0; c0 < sp.chunks; c0 += kMergeBatch) {
+        float lse[kMergeBatch];
+        f32x4 v0[kMergeBatch], v1[kMergeBatch];
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const bool in = c0 + i < sp.chunks;
+            const float* sl = pbase + (long long)(in ? c0 + i : c0) * kSlot;
+            lse[i] = in ? sl[kGqa * kHeadDim + h] : -DV_INF;
+            v0[i] = ld16f(sl + h * kHeadDim + d0);
+            v1[i] = ld16f(sl + h * kHeadDim + d0 + 4);
+        }
+        float bm = m;
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) bm = fmaxf(bm, lse[i]);
+        if (bm == -DV_INF) continue;
+        const float scl = __builtin_amdgcn_exp2f(m - bm);  // m == -inf -> 0
+        wsum *= scl;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc8[e] *= scl;
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const float wgt = __builtin_amdgcn_exp2f(lse[i] - bm);  // empty chunk (-inf) -> 0
+            wsum += wgt;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                acc8[q] += wgt * v0[i][q];
+                acc8[4 + q] += wgt * v1[i][q];
+            }
+        }
+        m = bm;
+    }
+    store8<kF32>(outp, acc8, wsum > 0.0f ? 1.0f / wsum : 0.0f);
+}
+
+// Per-call flag tags: splitmix64 of a process-wide call counter, 48 bits, nonzero.
+unsigned long long next_tag() {
+    static std::atomic<unsigned long long> calls{0x5eed5eedull};
+    unsigned long long z = calls.fetch_add(0x9e3779b97f4a7c15ull, std::memory_order_relaxed);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    z &= (1ull << 48) - 1ull;
+    return z ? z : 1ull;
+}
+
+size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+}  // namespace small
+
+int small_chunks(int F, const int* toks) {
+    if (F < 1 || F > kMaxFragArgs) return -1;
+    long long c = 0;
+    for (int f = 0; f < F; ++f) c += toks[f] > 0 ? (toks[f] + kSmallChunk - 1) / kSmallChunk : 1;
+    return c <= kSmallMaxChunks ? (int)c : -1;
+}
+
+size_t small_workspace_bytes(long long items, int chunks) {
+    if (items <= 0 || chunks <= 1) return 0;
+    return small::align256((size_t)items * chunks * sizeof(unsigned long long)) +
+           (size_t)items * chunks * small::kSlot * sizeof(float);
+}
+
+hipError_t launch_small(int dtype, int qmode, SmallParams& p, void* workspace, hipStream_t stream) {
+    if (dtype != kF32 || (qmode != kQPre && qmode != kQRotFull)) return hipErrorInvalidValue;
+    const long long items = (long long)p.d.W * p.d.S * p.d.Hkv;
+    if (items <= 0) return hipSuccess;
+    const long long grid = items * p.chunks;
+    if (p.chunks < 1 || p.chunks > kSmallMaxChunks || grid > 0x7fffffffll) return hipErrorInvalidValue;
+    p.flags = reinterpret_cast<unsigned long long*>(workspace);
+    p.part = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
+                                      small::align256((size_t)items * p.chunks * sizeof(unsigned long long)));
+    p.tag = small::next_tag();
+    if (qmode == kQRotFull)
+        hipLaunchKernelGGL((small::dv_small32<kQRotFull>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((small::dv_small32<kQPre>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    return hipGetLastError();
+}
+
+}  // namespace dv
