@@ -8,7 +8,8 @@ implemented by hand-written HIP kernels for gfx950 behind a C ABI
 
 Importing the package registers ``torch.ops.libdvatt.*`` from the in-tree
 ``_libdvatt.so``.  There is no fallback: if the native libraries are missing the
-import fails (build them with ``python -m dvattention_amd._build``).
+import fails (build them with ``python dvattention_amd/_build.py``, which runs
+without importing the package).
 """
 from __future__ import annotations
 
@@ -25,7 +26,7 @@ def _load_ops() -> None:
     if not os.path.exists(TORCH_OPS_LIBRARY) or not os.path.exists(CAPI_LIBRARY):
         raise ImportError(
             "dvattention_amd: native libraries are not built "
-            f"({TORCH_OPS_LIBRARY}, {CAPI_LIBRARY}); run `python -m dvattention_amd._build`")
+            f"({TORCH_OPS_LIBRARY}, {CAPI_LIBRARY}); run `python dvattention_amd/_build.py`")
     if not hasattr(torch.ops.libdvatt, "dvattn_paged_sdpa"):
         torch.ops.load_library(TORCH_OPS_LIBRARY)
 

@@ -6,7 +6,8 @@
   (csrc/torch_ops.cpp), a thin host-only C++ layer over the C ABI, compiled with
   g++ against the installed torch and linked to ``libdvattn_amd.so``.
 
-Run ``python -m dvattention_amd._build`` (or ``__graft_entry__.build()``).
+Run ``python dvattention_amd/_build.py`` (or ``__graft_entry__.build()``); both load
+this file without importing the package, whose import needs the libraries.
 Both libraries land next to this file so they travel with the source tree.
 """
 from __future__ import annotations

@@ -66,7 +66,7 @@ def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
         if not os.path.exists(LIBRARY):
-            raise ImportError(f"{LIBRARY} is not built; run `python -m dvattention_amd._build`")
+            raise ImportError(f"{LIBRARY} is not built; run `python dvattention_amd/_build.py`")
         L = ctypes.CDLL(LIBRARY)
         L.dvattn_last_error.restype = ctypes.c_char_p
         L.dvattn_last_error.argtypes = []
