@@ -135,9 +135,9 @@ __device__ inline void issue32(const DecodeParams& p, const KvCtx& c, const Page
         const unsigned char* kp = okb[kb] ? c.k + (row + g * 4) * 4 : g_zero_row + g * 16;
         const unsigned char* vp = okb[kb] ? c.v + (row + g * 4) * 4 : g_zero_row + g * 16;
 #pragma unroll
-        for (int cc = 0; cc < 8; ++cc) b.k[kb][cc] = ld16f(kp + cc * 64);
+        for (int cc = 0; cc < 8; ++cc) b.k[kb][cc] = ld16f_nt(kp + cc * 64);
 #pragma unroll
-        for (int cc = 0; cc < 8; ++cc) b.v[kb][cc] = ld16f(vp + cc * 64);
+        for (int cc = 0; cc < 8; ++cc) b.v[kb][cc] = ld16f_nt(vp + cc * 64);
     }
     b.mask = (uint32_t)(ballot(okb[0]) & 0xffffu) | ((uint32_t)(ballot(okb[1]) & 0xffffu) << 16);
 }

@@ -89,6 +89,8 @@ typedef __attribute__((address_space(1))) const u32x4 gu32x4;
 typedef __attribute__((address_space(1))) const f32x4 gf32x4;
 __device__ inline u32x4 ld16(const void* p) { return *(gu32x4*)(p); }
 __device__ inline f32x4 ld16f(const void* p) { return *(gf32x4*)(p); }
+// Non-temporal (streaming) 16-byte load, for K/V rows read once per call.
+__device__ inline f32x4 ld16f_nt(const void* p) { return __builtin_nontemporal_load((gf32x4*)(p)); }
 
 // Transposed LDS read (gfx950 ds_read_b64_tr_b16).  Within each 16-lane block,
 // result lane i, element j = the 16-bit word (i % 4) at the address supplied by
@@ -134,8 +136,12 @@ __device__ inline uint32_t lds_addr(const void* p) {
 // m0 needs one wait state before an LDS-DMA instruction reads it (the compiler's
 // hazard recognizer inserts the same s_nop for its own global_load_lds); without
 // it the first lanes of the load can use the previous m0.
+// The load is non-temporal (nt): every K/V row and query row staged this way
+// is read once per call, and streaming reads with nt reach ~7.0 TB/s on MI355X
+// against ~6.3 TB/s with the default policy (measured with a plain full-chip
+// read); the decode's paged read rate rose from 5.7 to 6.5 TB/s with it.
 __device__ inline void dma16(const void* gptr, uint32_t lds_base) {
-    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr), "s"(lds_base)
+    asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(gptr), "s"(lds_base)
                  : "memory", "m0");
 }
 

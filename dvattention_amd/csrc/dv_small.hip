@@ -179,14 +179,14 @@ __global__ __launch_bounds__(256) void dv_small32(const SmallParams sp) {
         const int key = k0 + n;
         const float* kp = (key < fd.L ? kbase + (long long)key * kHeadDim : zrow) + g * 4;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) kr[c] = ld16f(kp + c * 16);
+        for (int c = 0; c < 8; ++c) kr[c] = ld16f_nt(kp + c * 16);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int key = k0 + g * 4 + i;
         const float* vp = (key < fd.L ? vbase + (long long)key * kHeadDim : zrow) + n * 4;
-        vr[i][0] = ld16f(vp);
-        vr[i][1] = ld16f(vp + 64);
+        vr[i][0] = ld16f_nt(vp);
+        vr[i][1] = ld16f_nt(vp + 64);
     }
     store_query(qst, sm.q, sm.cs, sm.sn, sm.spare);
     __syncthreads();
