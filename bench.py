@@ -52,7 +52,16 @@ def replicas_for(wl_bytes: int, max_replicas: int = 4096) -> int:
     return min(max_replicas, need)
 
 
-def time_config(i: int, steps: int, warmup: int, device) -> dict:
+# Configurations other than the headline time at least this much GPU work per
+# measurement (more calls than --steps when a call is short): a few tens of
+# calls of a 10 us call are dominated by the first launch's host latency.
+MIN_TIMED_US = 2000.0
+
+
+def time_config(i: int, steps: int, warmup: int, device, exact: bool = False) -> dict:
+    """Per-call time of configuration i.  exact: time exactly `steps` calls (the
+    headline); otherwise at least `steps` calls and at least MIN_TIMED_US of
+    work, estimated from the warm-up calls."""
     from dvattention_amd import workloads as WL
     first = WL.config(i, device=device, seed=1234)
     R = replicas_for(first.meta.get("kv_bytes", first.alg_bytes))
@@ -62,6 +71,14 @@ def time_config(i: int, steps: int, warmup: int, device) -> dict:
     for j in range(warmup):
         WL.run(wls[j % R], outs[j % R], rqs[j % R])
     torch.cuda.synchronize()
+    if not exact:
+        # 10 more untimed calls estimate the call time
+        t_w = time.perf_counter()
+        for j in range(10):
+            WL.run(wls[j % R], outs[j % R], rqs[j % R])
+        torch.cuda.synchronize()
+        est_us = (time.perf_counter() - t_w) * 1e6 / 10
+        steps = max(steps, min(4096, int(MIN_TIMED_US / max(est_us, 1.0)) + 1))
     stream = torch.cuda.current_stream()
     # (a) K back-to-back steps between two synchronisations (wall clock + events)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -93,6 +110,7 @@ def time_config(i: int, steps: int, warmup: int, device) -> dict:
         "op": first.op,
         "dtype": str(first.dtype).replace("torch.", ""),
         "replicas": R,
+        "steps": steps,
         "us_per_call": round(ms_step * 1e3, 2),
         "us_per_call_wall": round(wall * 1e6, 2),
         "kernel_us_mean": round(kern_ms * 1e3, 2),
@@ -164,6 +182,42 @@ def read_ceiling(i: int, steps: int, warmup: int, device) -> dict:
     torch.cuda.empty_cache()
     return {"config": i, "workload": first.name, "probe_us_per_call": round(us, 2), "kv_bytes": int(kv),
             "read_GBs": round(kv / (us * 1e-6) / 1e9, 1), "read_frac": round(kv / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+def plain_read(device, gib: int = 4, calls: int = 10) -> dict:
+    """A plain full-chip streaming read of a contiguous buffer (dv_probe.hip
+    `dvprobe_plain_read`: 16-byte loads, grid-stride), with non-temporal and with
+    default-policy loads: the part's read rate without paging, for scale."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(HERE, "dvattention_amd", "libdvattn_probe.so"))
+    lib.dvprobe_last_error.restype = ctypes.c_char_p
+    lib.dvprobe_plain_read.restype = ctypes.c_int
+    lib.dvprobe_plain_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_void_p,
+                                       ctypes.c_longlong, ctypes.c_void_p]
+    nbytes = gib << 30
+    buf = torch.ones(nbytes // 4, dtype=torch.int32, device=device)
+    sink = torch.empty(4 * 8192, dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream()
+    out = {"bytes": nbytes}
+    for nt in (1, 0):
+        def call():
+            if lib.dvprobe_plain_read(buf.data_ptr(), nbytes, nt, sink.data_ptr(), sink.numel(),
+                                      stream.cuda_stream) != 0:
+                raise RuntimeError(lib.dvprobe_last_error().decode())
+        for _ in range(3):
+            call()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(stream)
+        for _ in range(calls):
+            call()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / calls
+        out["nontemporal_GBs" if nt else "default_GBs"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+    del buf
+    torch.cuda.empty_cache()
+    return out
 
 
 def _time_calls(fn, n_inputs: int, steps: int, warmup: int) -> tuple:
@@ -358,14 +412,17 @@ def main() -> int:
             rows[-1]["decode_kernel_us"] = dec["kernel_us_mean"]
             log(f"[bench] read probe cfg{i}: {rows[-1]['probe_us_per_call']} us/call, {rows[-1]['read_GBs']} GB/s "
                 f"(decode {dec['us_per_call']} us/call)")
-        print(json.dumps({"read_ceiling": rows}), flush=True)
+        plain = plain_read(device)
+        log(f"[bench] plain streaming read of {plain['bytes'] >> 30} GiB: {plain['nontemporal_GBs']} GB/s "
+            f"non-temporal, {plain['default_GBs']} GB/s default policy")
+        print(json.dumps({"read_ceiling": rows, "plain_read": plain}), flush=True)
         return 0
     cfgs = [int(x) for x in args.configs.split(",") if x]
     if 2 not in cfgs:
         cfgs = [2] + cfgs
     per = {}
     for i in cfgs:
-        r = time_config(i, args.steps, args.warmup, device)
+        r = time_config(i, args.steps, args.warmup, device, exact=(i == 2))
         per[i] = r
         log(f"[bench] cfg{i} {r['workload']}: {r['us_per_call']} us/call (events, back-to-back), "
             f"kernel {r['kernel_us_mean']} us, {r['achieved_GBs']} GB/s = {100 * r['hbm_frac']:.1f}% HBM, "

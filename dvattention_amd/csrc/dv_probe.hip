@@ -1,4 +1,6 @@
-// Paged-read probe (libdvattn_probe.so, used by `bench.py --read-ceiling`):
+// Read probes (libdvattn_probe.so, used by `bench.py --read-ceiling`).
+//
+// Paged-read probe:
 // the 16-bit decode kernel's K/V stream with the attention taken out.  It runs
 // the decode's work split (run_schedule with the same start cost, XCD skew and
 // minimum range), fills the same per-wave page-id cache and streams every
@@ -87,6 +89,29 @@ __global__ __launch_bounds__(256) void dv_read_probe(const DecodeParams p, unsig
         if (wv < HPW) acc += read_piece(p, wlds, row, hg * HPW + wv, v0, v1, rk);
     });
     if ((threadIdx.x & 63) == 0) sink[blockIdx.x * kMaxWavesPerWg + wv] = acc;
+}
+
+// Plain streaming read of a contiguous buffer (16-byte loads, 8 per lane in
+// flight per iteration, grid-stride), with the non-temporal or the default
+// cache policy: the part's read rate for an access pattern with no paging, to
+// set the paged probe's rate against.
+template <bool NT>
+__global__ __launch_bounds__(256) void dv_plain_read(const u32x4* __restrict__ buf, long long n16, unsigned* sink) {
+    constexpr int U = 8;
+    long long i = (long long)blockIdx.x * 256 * U + threadIdx.x;
+    const long long stride = (long long)gridDim.x * 256 * U;
+    unsigned acc = 0;
+    for (; i + (U - 1) * 256 < n16; i += stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const gu32x4* q = (const gu32x4*)(buf + i + u * 256);
+            v[u] = NT ? __builtin_nontemporal_load(q) : *q;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
+    }
+    if ((threadIdx.x & 63) == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = acc;
 }
 
 thread_local const char* g_msg = "";
@@ -181,6 +206,31 @@ __attribute__((visibility("default"))) int dvprobe_paged_read(int dtype, const i
         return -1;
     }
     hipLaunchKernelGGL(dv_read_probe, dim3(p.nwg), dim3(p.hpw * kWave), lds, (hipStream_t)stream, p, sink);
+    if (hipGetLastError() != hipSuccess) {
+        g_msg = "probe: launch failed";
+        return -1;
+    }
+    g_msg = "";
+    return 0;
+}
+
+// Reads `bytes` (a multiple of 32 KiB, 16-byte aligned) of `buf` once with
+// 16-byte loads, non-temporal when `nontemporal` is set; `sink` receives 4 words
+// per workgroup (sink_words >= 4 * 8192).  Returns 0, or -1 with a message.
+__attribute__((visibility("default"))) int dvprobe_plain_read(const void* buf, size_t bytes, int nontemporal,
+                                                               unsigned* sink, long long sink_words, void* stream) {
+    using namespace dv;
+    constexpr int kGrid = 8192;
+    if (!buf || !sink || (bytes & 32767) || ((uintptr_t)buf & 15) || sink_words < 4ll * kGrid) {
+        g_msg = "probe: plain read needs a 16-byte aligned buffer of a multiple of 32 KiB and 4 x 8192 sink words";
+        return -1;
+    }
+    const long long n16 = (long long)(bytes / 16);
+    const u32x4* b = reinterpret_cast<const u32x4*>(buf);
+    if (nontemporal)
+        hipLaunchKernelGGL(dv_plain_read<true>, dim3(kGrid), dim3(256), 0, (hipStream_t)stream, b, n16, sink);
+    else
+        hipLaunchKernelGGL(dv_plain_read<false>, dim3(kGrid), dim3(256), 0, (hipStream_t)stream, b, n16, sink);
     if (hipGetLastError() != hipSuccess) {
         g_msg = "probe: launch failed";
         return -1;
