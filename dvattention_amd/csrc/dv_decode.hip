@@ -680,21 +680,28 @@ __global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
 
 constexpr int kMergeBatch = 8;  // pieces whose loads are in flight together
 
-// Block (segment, KV head) with 256 threads: thread t handles query head t/16,
-// dims [(t%16)*8, +8).  count == 1: already final; count == 0: no visible key ->
-// zeros (paged_kernel_v21.cuh:318); otherwise the base-2-LSE-weighted sum of the
-// pieces' normalised outputs (paged_kernel_v21.cuh:325-364).
+// Block (segment, KV head, quarter of the head dims) with one wave: thread t
+// handles query head t/4, dims [q*32 + (t%4)*8, +8).  count == 1: already final;
+// count == 0: no visible key -> zeros (paged_kernel_v21.cuh:318); otherwise the
+// base-2-LSE-weighted sum of the pieces' normalised outputs
+// (paged_kernel_v21.cuh:325-364).  The quarters spread a long segment's
+// partials (up to ~40 pieces x 8 KiB per KV head) over four CUs: one CU reads
+// at only ~50-100 GB/s, which set the merge time of segments with many pieces.
+constexpr int kMergeQuarters = 4;
+
 template <int DT, int RM>
-__global__ __launch_bounds__(256) void dv_merge(const DecodeParams p) {
+__global__ __launch_bounds__(64) void dv_merge(const DecodeParams p) {
     using raw = typename Tr<DT>::raw;
-    const int sg = blockIdx.x / p.hpw;
-    const int wi = blockIdx.x - sg * p.hpw;
+    const int qi = blockIdx.x % kMergeQuarters;
+    const int sw = blockIdx.x / kMergeQuarters;
+    const int sg = sw / p.hpw;
+    const int wi = sw - sg * p.hpw;
     const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
     if (cnt == 1) return;
     const int NHG = p.Hkv / p.hpw;
     const int tid = threadIdx.x;
-    const int n = tid >> 4;
-    const int d = (tid & 15) * 8;
+    const int n = tid >> 2;
+    const int d = qi * 32 + (tid & 3) * 8;
     const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
     const int row = p.row_begin + r;
     const int h = (hg * p.hpw + wi) * kGqa + n;
@@ -825,7 +832,7 @@ hipError_t launch_one(DecodeParams p, int device, long long max_wg, long long ca
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return note_site(e, "launch decode");
     const int nseg = p.nrows * (p.Hkv / p.hpw);
-    hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg * p.hpw), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg * p.hpw * kMergeQuarters), dim3(kWave), 0, stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return note_site(e, "launch dv_merge");
     return hipSuccess;
