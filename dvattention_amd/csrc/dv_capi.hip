@@ -391,17 +391,26 @@ int small_path_chunks(int dtype, const dvattn_shape* s, const int* fragment_toke
     if (env && env[0] == '0') return -1;
     const bool require = env && strcmp(env, "require") == 0;
     int chunks = -1;
-    if (dtype == DVATTN_F32 && s->F >= 1 && s->F <= dv::kMaxFragArgs && (!rotating || s->rotary_dim % 8 == 0)) {
+    if (s->F >= 1 && s->F <= dv::kMaxFragArgs && (!rotating || s->rotary_dim % 8 == 0)) {
         chunks = dv::small_chunks(s->F, fragment_tokens);
         const long long items = (long long)s->W * s->S * s->Hkv;
+        // Views of one chunk each need no merge.  Otherwise every workgroup
+        // pays the merge protocol's fences, whose cost grows with the number of
+        // workgroups: past items x chunks = small_max_merged() the general path
+        // (rotation, decode and merge launches) is faster (measured crossover
+        // about 190 workgroups for fp32, about 110 for 16-bit types, whose
+        // general path is faster).
+        if (chunks > 1 && items * chunks > dv::small_max_merged(dtype)) chunks = -1;
         if (chunks >= 1 && dv::small_workspace_bytes(items, chunks) > dvattn_sdpa_workspace_size(dtype, s, -1))
             chunks = -1;
     }
     if (chunks < 1 && require) {
         fail(DVATTN_ERR_UNSUPPORTED,
-             "DVATTN_SMALL_PATH=require: the single-launch path takes fp32 calls of 1-%d views with at most %d "
-             "chunks of %d keys per row (and rotary_dim %% 8 == 0 when it rotates)",
-             dv::kMaxFragArgs, dv::kSmallMaxChunks, dv::kSmallChunk);
+             "DVATTN_SMALL_PATH=require: the single-launch path takes calls of 1-%d views with at most %d "
+             "chunks of %d keys per row, and at most %d (fp32) or %d (16-bit) workgroups in all when a row "
+             "has more than one chunk (one per row, KV head and chunk); rotary_dim %% 8 == 0 when it rotates",
+             dv::kMaxFragArgs, dv::kSmallMaxChunks, dv::kSmallChunk, dv::small_max_merged(DVATTN_F32),
+             dv::small_max_merged(DVATTN_BF16));
         *refused = true;
     }
     return chunks;

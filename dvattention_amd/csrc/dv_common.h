@@ -85,6 +85,8 @@ struct DecodeParams {
 // merges its chunks.  Rotating mode needs rotary_dim % 8 == 0.
 constexpr int kSmallChunk = 64;       // tensor keys per workgroup (16 per wave)
 constexpr int kSmallMaxChunks = 64;   // chunks per (row, KV head): up to 4096 keys
+// Most workgroups (items x chunks) of a call whose rows have several chunks.
+inline int small_max_merged(int dtype) { return dtype == kF32 ? 160 : 96; }
 
 struct SmallParams {
     DecodeParams d;                   // out, loc, q, cosv, sinv, fl, frags, l2scale, F, W, S, Hq, Hkv, R
@@ -185,7 +187,7 @@ inline bool use_chunk(int dtype, int S) { return S >= 2 && dtype != kF32; }
 size_t chunk_workspace_bytes(int W, int S, int Hkv, int device);
 hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& base, long long max_keys_per_group,
                         void* workspace, size_t ws_bytes, hipStream_t stream);
-// Single-launch path (fp32 contiguous views): chunks per item for F views of
+// Single-launch path (contiguous views, any dtype): chunks per item for F views of
 // fragment_tokens toks, or -1 when the views are too many or too long; the
 // workspace it needs for `items` (row, KV head) items; the launch (qmode kQPre
 // or kQRotFull).  launch_small fills p.part / p.flags / p.tag from the workspace.

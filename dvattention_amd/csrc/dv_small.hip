@@ -1,6 +1,6 @@
 // Single-launch attention for short contiguous views (ops dvattn_sdpa and
-// dvattn_fused, fp32): the query rotation, the attention and the merge of the
-// key chunks in one kernel, where the general path (dv_decode.hip) takes a
+// dvattn_fused, fp32 / fp16 / bf16): the query rotation, the attention and the
+// merge of the key chunks in one kernel, where the general path (dv_decode.hip) takes a
 // rotation launch, a decode launch whose every workgroup first computes the
 // whole work split, and a merge launch.  Same operator semantics as
 // src/kernels/kernel_v21.cuh:17-414 and src/binding.cu:356-372 (reference
@@ -17,7 +17,10 @@
 //    MFMA (16x16x4, dims as the reduction index), the softmax of each head over
 //    its keys, and O = P V with V read straight from global memory (a lane
 //    loads 4 consecutive dims, so output column n of the t-th MFMA is dim
-//    64 b + 4 n + t).  The four waves are combined in LDS.
+//    64 b + 4 n + t).  The four waves are combined in LDS.  16-bit inputs are
+//    widened to fp32 in registers (exactly) and take the same fp32 arithmetic;
+//    the rotated query is rounded to the storage type first, as the
+//    reference's rq tensor is, and the output is rounded once at the end.
 //  * Merge: a workgroup stores its chunk's normalised output and base-2
 //    log-sum-exp, then raises its arrival flag and reads the flags of all the
 //    item's chunks; a workgroup that finds them all raised merges every chunk
@@ -26,9 +29,17 @@
 //    call (a word left by an earlier call, or arbitrary workspace bytes, hold
 //    another value); a merging workgroup lowers the item's flags to zero, so
 //    the same tag replayed (a captured graph) starts from lowered flags too.
+//  * Cost of the merge protocol: the agent-scope fences write back and
+//    invalidate the L2 of the workgroup's XCD, work that grows with the
+//    number of workgroups in flight (measured: +2-3 us at 64 workgroups of
+//    several chunks, +18 us at 256).  The host therefore sends a call here
+//    only when its views fit one chunk each (no merge, no fence) or when
+//    items x chunks is small (dv_capi.hip: small_path_chunks); larger calls
+//    take the general path.
 #include <string.h>
 
 #include <atomic>
+#include <type_traits>
 
 #include "dv_common.h"
 #include "dv_device.h"
@@ -44,7 +55,8 @@ constexpr int kMergeBatch = 8;                       // partials loaded together
 static_assert(kKeysPerWave == 16, "one 16-key MFMA block per wave");
 
 struct Smem {
-    float q[kGqa][kHeadDim];          // the item's query rows (unrotated in rotating mode)
+    float q[kGqa][kHeadDim];          // the item's query rows (unrotated in rotating mode; 16-bit
+                                      // types: [kGqa][kHeadDim] raw elements in the first half)
     float cs[kHeadDim], sn[kHeadDim]; // cos / sin row (rotating mode)
     float spare[4];                   // written by threads without a cos/sin part (store_query)
     float o[kWaves][kGqa][kHeadDim];  // each wave's unnormalised output
@@ -52,6 +64,47 @@ struct Smem {
     float l[kWaves][kGqa];            // its per-head sum of exp2(score - max)
     int last;
 };
+
+// Four 16-bit values (8 bytes) widened to fp32 (exact).
+template <int DT>
+__device__ inline f32x4 widen4(u32x2 v) {
+    if constexpr (DT == kBF16) {
+        return f32x4{__uint_as_float(v[0] << 16), __uint_as_float(v[0] & 0xffff0000u), __uint_as_float(v[1] << 16),
+                     __uint_as_float(v[1] & 0xffff0000u)};
+    } else {
+        // the words are copied to scalars first: a bit cast of a vector
+        // element (v[1], v.y) is compiled into a cast of element 0
+        const uint32_t lo = v[0], hi = v[1];
+        const f16x2 a = __builtin_bit_cast(f16x2, lo);
+        const f16x2 b = __builtin_bit_cast(f16x2, hi);
+        return f32x4{(float)a[0], (float)a[1], (float)b[0], (float)b[1]};
+    }
+}
+
+typedef __attribute__((address_space(1))) const u32x2 gu32x2;
+
+// Four consecutive elements of a K/V row as loaded (fp32: f32x4; 16-bit: two
+// words), widened where they are used: a conversion next to the loads is
+// scheduled between them, and the loads after it then wait for the earlier ones.
+template <int DT>
+using Run4 = typename std::conditional<DT == kF32, f32x4, u32x2>::type;
+
+// The run at element offset `e` of `row` (non-temporal: read once per call).
+template <int DT>
+__device__ inline Run4<DT> ld4_nt(const void* row, int e) {
+    if constexpr (DT == kF32)
+        return ld16f_nt(reinterpret_cast<const float*>(row) + e);
+    else
+        return __builtin_nontemporal_load((gu32x2*)(reinterpret_cast<const uint16_t*>(row) + e));
+}
+
+template <int DT>
+__device__ inline f32x4 run_f32(Run4<DT> r) {
+    if constexpr (DT == kF32)
+        return r;
+    else
+        return widen4<DT>(r);
+}
 
 // Query rows of the item, staged in LDS: thread t loads dims (t%16)*8 .. +7
 // of head t/16 (rotated queries [F,W,Hq,S,E] in kQPre mode, queries
@@ -61,20 +114,25 @@ struct Smem {
 // issued (store_query), so every global load of the workgroup is in flight
 // at once.
 struct QStage {
-    f32x4 a, b, c;
+    f32x4 a, b, c;  // fp32 query run (a, b) or 16-bit run (u), cos/sin run (c)
+    u32x4 u;
     bool trig;
 };
 
-template <int QM>
+template <int DT, int QM>
 __device__ inline QStage load_query(const DecodeParams& p, int w, int s, int f, int hkv) {
     const int tid = threadIdx.x;
     const int hh = tid >> 4, dd = (tid & 15) * 8;
     const long long qrow = QM == kQPre ? ((((long long)f * p.W + w) * p.Hq + hkv * kGqa + hh) * p.S + s) * kHeadDim
                                        : (((long long)w * p.Hq + hkv * kGqa + hh) * p.S + s) * kHeadDim;
-    const float* q = reinterpret_cast<const float*>(p.q) + qrow + dd;
     QStage r;
-    r.a = ld16f(q);
-    r.b = ld16f(q + 4);
+    if constexpr (DT == kF32) {
+        const float* q = reinterpret_cast<const float*>(p.q) + qrow + dd;
+        r.a = ld16f(q);
+        r.b = ld16f(q + 4);
+    } else {
+        r.u = ld16(reinterpret_cast<const uint16_t*>(p.q) + qrow + dd);
+    }
     const int j = tid & 63;
     r.trig = QM != kQPre && tid < 128 && j * 4 < p.R;
     // a select of the address rather than a branch around the load, so the
@@ -89,23 +147,40 @@ __device__ inline QStage load_query(const DecodeParams& p, int w, int s, int f, 
     return r;
 }
 
+template <int DT>
 __device__ inline void store_query(const QStage& r, float (*qs)[kHeadDim], float* cs, float* sn, float* spare) {
     const int tid = threadIdx.x;
     const int hh = tid >> 4, dd = (tid & 15) * 8;
-    *reinterpret_cast<f32x4*>(&qs[hh][dd]) = r.a;
-    *reinterpret_cast<f32x4*>(&qs[hh][dd + 4]) = r.b;
+    if constexpr (DT == kF32) {
+        *reinterpret_cast<f32x4*>(&qs[hh][dd]) = r.a;
+        *reinterpret_cast<f32x4*>(&qs[hh][dd + 4]) = r.b;
+    } else {
+        // stored as loaded: a conversion here is scheduled between the K/V
+        // loads, whose last ones then wait for the query
+        *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(qs) + hh * kHeadDim + dd) = r.u;
+    }
     // unconditional store (threads without a cos/sin part write the spare
     // slot): a conditional one lets the compiler sink the load into the branch
     float* dst = r.trig ? (tid < 64 ? cs : sn) + (tid & 63) * 4 : spare;
     *reinterpret_cast<f32x4*>(dst) = r.c;
 }
 
+// Dims d .. d+3 of staged query row n, as fp32.
+template <int DT>
+__device__ inline f32x4 staged_run(const float (*qs)[kHeadDim], int n, int d) {
+    if constexpr (DT == kF32)
+        return *reinterpret_cast<const f32x4*>(&qs[n][d]);
+    else
+        return widen4<DT>(*reinterpret_cast<const u32x2*>(reinterpret_cast<const uint16_t*>(qs) + n * kHeadDim + d));
+}
+
 // Query operand from the staged rows: lane (g, n) holds Q[n][c*16 + g*4 + 0..3],
 // c = 0..7 (the B operand of S^T).  Rotating mode applies the reference's rope
 // (src/rope.cuh:18-51) with the same roundings as rotate_run: separate fp32
-// products, then their difference or sum; dims >= R are copied.  Needs
-// rotary_dim % 8 == 0, so a run of 4 dims never straddles the two halves.
-template <int QM>
+// products, then their difference or sum, rounded to the storage type; dims
+// >= R are copied.  Needs rotary_dim % 8 == 0, so a run of 4 dims never
+// straddles the two halves.
+template <int DT, int QM>
 __device__ inline void query_operand(const DecodeParams& p, const float (*qs)[kHeadDim], const float* cs,
                                      const float* sn, f32x4 (&qB)[8]) {
 #pragma clang fp contract(off)
@@ -115,7 +190,7 @@ __device__ inline void query_operand(const DecodeParams& p, const float (*qs)[kH
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
         const int d = c * 16 + g * 4;
-        const f32x4 x = *reinterpret_cast<const f32x4*>(&qs[n][d]);
+        const f32x4 x = staged_run<DT>(qs, n, d);
         if constexpr (QM == kQPre) {
             qB[c] = x;
         } else {
@@ -123,7 +198,7 @@ __device__ inline void query_operand(const DecodeParams& p, const float (*qs)[kH
             const bool first = d < half;
             const int pd = rot ? (first ? d + half : d - half) : d;
             const int ci = rot ? (first ? d : pd) : 0;
-            const f32x4 xp = *reinterpret_cast<const f32x4*>(&qs[n][pd]);
+            const f32x4 xp = staged_run<DT>(qs, n, pd);
             const f32x4 cv = *reinterpret_cast<const f32x4*>(cs + ci);
             const f32x4 sv = *reinterpret_cast<const f32x4*>(sn + ci);
 #pragma unroll
@@ -131,7 +206,7 @@ __device__ inline void query_operand(const DecodeParams& p, const float (*qs)[kH
                 const float a = x[e] * cv[e];
                 const float b = xp[e] * sv[e];
                 const float y = first ? a - b : a + b;
-                qB[c][e] = rot ? y : x[e];
+                qB[c][e] = rot ? Tr<DT>::tof(Tr<DT>::fromf(y)) : x[e];
             }
         }
     }
@@ -149,8 +224,9 @@ __device__ inline void store8(void* dst, const float (&o)[8], float inv) {
     }
 }
 
-template <int QM>
-__global__ __launch_bounds__(256) void dv_small32(const SmallParams sp) {
+template <int DT, int QM>
+__global__ __launch_bounds__(256) void dv_small(const SmallParams sp) {
+    using raw = typename Tr<DT>::raw;
     __shared__ __align__(16) Smem sm;
     const DecodeParams& p = sp.d;
     const int item = blockIdx.x / sp.chunks;  // (query row, KV head)
@@ -165,47 +241,57 @@ __global__ __launch_bounds__(256) void dv_small32(const SmallParams sp) {
     const int tid = threadIdx.x;
     const int wv = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int k0 = (ci - sp.first_chunk[f]) * kSmallChunk + wv * kKeysPerWave;  // wave's first tensor key
-    const float* kbase = reinterpret_cast<const float*>(fd.k) + fd.bstride * w + (long long)hkv * fd.L * kHeadDim;
-    const float* vbase = reinterpret_cast<const float*>(fd.v) + fd.bstride * w + (long long)hkv * fd.L * kHeadDim;
-    const float* zrow = reinterpret_cast<const float*>(g_zero_row);
+    const raw* kbase = reinterpret_cast<const raw*>(fd.k) + fd.bstride * w + (long long)hkv * fd.L * kHeadDim;
+    const raw* vbase = reinterpret_cast<const raw*>(fd.v) + fd.bstride * w + (long long)hkv * fd.L * kHeadDim;
+    const raw* zrow = reinterpret_cast<const raw*>(g_zero_row);
     const int vis = view_vis<kKvContig>(p, f, row_loc<kRowWS>(p, row, f));
 
     // ---- loads, all issued together: the query rows and cos/sin (staged in
     // LDS), K (key k0 + n, dims c*16 + g*4 + 0..3) and V (key k0 + g*4 + i,
     // dims 64 b + 4 n + 0..3) to registers; keys past the tensor read the zero row
-    const QStage qst = load_query<QM>(p, w, s, f, hkv);
-    f32x4 kr[8], vr[4][2];
+    const QStage qst = load_query<DT, QM>(p, w, s, f, hkv);
+    Run4<DT> kr[8], vr[4][2];
     {
         const int key = k0 + n;
-        const float* kp = (key < fd.L ? kbase + (long long)key * kHeadDim : zrow) + g * 4;
+        const raw* kp = key < fd.L ? kbase + (long long)key * kHeadDim : zrow;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) kr[c] = ld16f_nt(kp + c * 16);
+        for (int c = 0; c < 8; ++c) kr[c] = ld4_nt<DT>(kp, c * 16 + g * 4);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const int key = k0 + g * 4 + i;
-        const float* vp = (key < fd.L ? vbase + (long long)key * kHeadDim : zrow) + n * 4;
-        vr[i][0] = ld16f_nt(vp);
-        vr[i][1] = ld16f_nt(vp + 64);
+        const raw* vp = key < fd.L ? vbase + (long long)key * kHeadDim : zrow;
+        vr[i][0] = ld4_nt<DT>(vp, n * 4);
+        vr[i][1] = ld4_nt<DT>(vp, 64 + n * 4);
     }
-    store_query(qst, sm.q, sm.cs, sm.sn, sm.spare);
+    // nothing that uses a loaded value is scheduled above the last load
+    __builtin_amdgcn_sched_barrier(0);
+    store_query<DT>(qst, sm.q, sm.cs, sm.sn, sm.spare);
     __syncthreads();
     f32x4 qB[8];
-    query_operand<QM>(p, sm.q, sm.cs, sm.sn, qB);
+    query_operand<DT, QM>(p, sm.q, sm.cs, sm.sn, qB);
     if (QM == kQRotFull && wv == 0 && ci == sp.first_chunk[f]) {
         // the view's rotated query, as dvattn_rope writes it
-        float* rq = reinterpret_cast<float*>(sp.rq) +
-                    ((((long long)f * p.W + w) * p.Hq + hkv * kGqa + n) * p.S + s) * kHeadDim + g * 4;
+        raw* rq = reinterpret_cast<raw*>(sp.rq) +
+                  ((((long long)f * p.W + w) * p.Hq + hkv * kGqa + n) * p.S + s) * kHeadDim + g * 4;
 #pragma unroll
-        for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(rq + c * 16) = qB[c];
+        for (int c = 0; c < 8; ++c) {
+            if constexpr (DT == kF32)
+                *reinterpret_cast<f32x4*>(rq + c * 16) = qB[c];
+            else  // exact: the values are rounded to the storage type already
+                *reinterpret_cast<u32x2*>(rq + c * 16) =
+                    u32x2{pack2<DT>(qB[c][0], qB[c][1]), pack2<DT>(qB[c][2], qB[c][3])};
+        }
     }
 
     // ---- S^T: lane (g, n) holds keys k0 + g*4 + i of head n
     f32x4 sc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 8; ++c)
+    for (int c = 0; c < 8; ++c) {
+        const f32x4 kc = run_f32<DT>(kr[c]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sc = Tr<kF32>::mma1(kr[c][j], qB[c][j], sc);
+        for (int j = 0; j < 4; ++j) sc = Tr<kF32>::mma1(kc[j], qB[c][j], sc);
+    }
     float pr[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) pr[i] = k0 + g * 4 + i < vis ? sc[i] * p.l2scale : -DV_INF;
@@ -225,9 +311,11 @@ __global__ __launch_bounds__(256) void dv_small32(const SmallParams sp) {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < 2; ++b) {
+            const f32x4 vv = run_f32<DT>(vr[i][b]);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) acc[b][t] = Tr<kF32>::mma1(pr[i], vr[i][b][t], acc[b][t]);
+            for (int t = 0; t < 4; ++t) acc[b][t] = Tr<kF32>::mma1(pr[i], vv[t], acc[b][t]);
+        }
     mfma_settle(reinterpret_cast<f32x4(&)[8]>(acc));
 #pragma unroll
     for (int b = 0; b < 2; ++b)
@@ -265,9 +353,9 @@ __global__ __launch_bounds__(256) void dv_small32(const SmallParams sp) {
         }
     }
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    float* outp = reinterpret_cast<float*>(p.out) + (((long long)w * p.Hq + hkv * kGqa + h) * p.S + s) * kHeadDim + d0;
+    raw* outp = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + hkv * kGqa + h) * p.S + s) * kHeadDim + d0;
     if (sp.chunks == 1) {
-        store8<kF32>(outp, o, inv);
+        store8<DT>(outp, o, inv);
         return;
     }
     float* slot = sp.part + ((long long)item * sp.chunks + ci) * kSlot;
@@ -336,7 +424,7 @@ __global__ __launch_bounds__(256) void dv_small32(const SmallParams sp) {
         }
         m = bm;
     }
-    store8<kF32>(outp, acc8, wsum > 0.0f ? 1.0f / wsum : 0.0f);
+    store8<DT>(outp, acc8, wsum > 0.0f ? 1.0f / wsum : 0.0f);
 }
 
 // Per-call flag tags: splitmix64 of a process-wide call counter, 48 bits, nonzero.
@@ -367,8 +455,17 @@ size_t small_workspace_bytes(long long items, int chunks) {
            (size_t)items * chunks * small::kSlot * sizeof(float);
 }
 
+template <int DT>
+void launch_small_dt(int qmode, const SmallParams& p, long long grid, hipStream_t stream) {
+    if (qmode == kQRotFull)
+        hipLaunchKernelGGL((small::dv_small<DT, kQRotFull>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    else
+        hipLaunchKernelGGL((small::dv_small<DT, kQPre>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+}
+
 hipError_t launch_small(int dtype, int qmode, SmallParams& p, void* workspace, hipStream_t stream) {
-    if (dtype != kF32 || (qmode != kQPre && qmode != kQRotFull)) return hipErrorInvalidValue;
+    if ((dtype != kF32 && dtype != kF16 && dtype != kBF16) || (qmode != kQPre && qmode != kQRotFull))
+        return hipErrorInvalidValue;
     const long long items = (long long)p.d.W * p.d.S * p.d.Hkv;
     if (items <= 0) return hipSuccess;
     const long long grid = items * p.chunks;
@@ -377,10 +474,9 @@ hipError_t launch_small(int dtype, int qmode, SmallParams& p, void* workspace, h
     p.part = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
                                       small::align256((size_t)items * p.chunks * sizeof(unsigned long long)));
     p.tag = small::next_tag();
-    if (qmode == kQRotFull)
-        hipLaunchKernelGGL((small::dv_small32<kQRotFull>), dim3((unsigned)grid), dim3(256), 0, stream, p);
-    else
-        hipLaunchKernelGGL((small::dv_small32<kQPre>), dim3((unsigned)grid), dim3(256), 0, stream, p);
+    if (dtype == kF32) launch_small_dt<kF32>(qmode, p, grid, stream);
+    else if (dtype == kF16) launch_small_dt<kF16>(qmode, p, grid, stream);
+    else launch_small_dt<kBF16>(qmode, p, grid, stream);
     return hipGetLastError();
 }
 
