@@ -6,23 +6,24 @@
 // paged_kernel_v21.cuh:391); here each K/V row is read once per block of 16
 // tokens.
 //
-//  * Workgroup = four waves, one per SIMD, on one (sequence, 16-token block,
+//  * Workgroup = eight waves, two per SIMD, on one (sequence, 16-token block,
 //    KV head) and a contiguous range of its visible keys.  Wave w owns tokens
-//    4w .. 4w+3: four 16-row query tiles (16 heads each), so a K/V stage read
-//    from LDS feeds 64 query rows.
+//    2w and 2w+1: two 16-row query tiles (16 heads each), so a K/V stage read
+//    from LDS feeds 32 query rows per wave and 256 per workgroup.
 //  * K/V pages stream through an 8-stage LDS ring filled by direct-to-LDS loads
-//    (global_load_lds_dwordx4): 32 keys x 256 B of K and of V per stage, one
-//    quarter issued by each wave, seven stages ahead of the one computed,
-//    completion tracked with vmcnt and one workgroup barrier per stage.
+//    (global_load_lds_dwordx4, non-temporal): 32 keys x 256 B of K and of V per
+//    stage, one eighth issued by each wave, seven stages ahead of the one
+//    computed, completion tracked with vmcnt and one workgroup barrier per stage.
 //  * Per stage and tile: S^T = K Q^T on 16x16x32 MFMA (8 per tile), online
 //    softmax per query row, O^T += V^T P^T (8 MFMA per tile, 16 for fp16: see
 //    p_operands); the K and V^T operands of a stage are read from LDS once per
-//    wave and kept in registers for its four tiles.
-//  * MFMA / VALU overlap inside the wave: the tiles form two groups (A = 0, 1;
-//    B = 2, 3) that run half a stage apart.  Each half-stage issues one group's
-//    MFMAs (S of B and P V of B's previous stage, or P V of A and S of A's next
-//    stage) while the other group's softmax runs on the VALU, so the two use
-//    disjoint registers and the matrix core stays busy during the softmax.
+//    wave and kept in registers for both tiles.
+//  * MFMA / VALU overlap inside the wave: the two tiles (A = 0, B = 1) run half
+//    a stage apart.  Each half-stage issues one tile's MFMAs (S of B and P V of
+//    B's previous stage, or P V of A and S of A's next stage) while the other
+//    tile's softmax runs on the VALU, so the two use disjoint registers and the
+//    matrix core has work during the softmax; the second wave on the SIMD fills
+//    what one wave's dependences leave idle.
 //  * Rows are causal-masked per token (key l visible iff l <= locations[f,w,s]).
 //  * The balanced split / LSE merge is the decode kernel's (equal key chunks per
 //    workgroup, fp32 partial slots, dv_merge_chunk).
