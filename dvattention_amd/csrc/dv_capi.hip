@@ -3,9 +3,11 @@
 // rejects the shapes/dtypes it silently ignored, and launches the gfx950
 // kernels on the caller's stream.  No exception crosses this boundary.
 #include <stdarg.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <string.h>
 
+#include <initializer_list>
 #include <mutex>
 #include <vector>
 
@@ -81,6 +83,27 @@ dvattn_status check_pages(const dvattn_shape* s) {
 
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
+// The attention kernels move queries, outputs, cache and view rows and partial
+// results as 16-byte vectors and LDS DMAs, update 8-byte merge flags in the
+// workspace atomically and read the int32 / fp32 arrays as 4-byte words (the
+// reference's kernels load 16-byte vectors too, paged_kernel_v21.cuh:58-62,
+// unchecked).  A pointer off that alignment is refused here instead of reaching
+// a kernel.  Null pointers pass: the null checks are separate.
+struct Aligned {
+    const void* ptr;
+    const char* name;
+    unsigned align;
+};
+
+unsigned elem_bytes(int dtype) { return dtype == DVATTN_F32 ? 4u : 2u; }
+
+dvattn_status check_aligned(std::initializer_list<Aligned> ptrs) {
+    for (const Aligned& a : ptrs)
+        if ((uintptr_t)a.ptr & (a.align - 1))
+            return fail(DVATTN_ERR_INVALID, "%s must be %u-byte aligned (got %p)", a.name, a.align, a.ptr);
+    return DVATTN_OK;
+}
+
 // ---- static scratch of dvattn_paged_sdpa_noalloc ------------------------------
 // Device memory for the partial results and merge directory of the paged entry
 // point, for callers that cannot allocate.  Each GPU the library runs on holds
@@ -149,6 +172,11 @@ dvattn_status dvattn_paged_sdpa(int dtype, void* out, float scale, const int* lo
         return fail(DVATTN_ERR_INVALID, "null locations / fragment_lengths / cos / sin pointer");
     if (s->num_blocks > 0 && (!k_cache || !v_cache)) return fail(DVATTN_ERR_INVALID, "null k/v cache pointer");
     if (s->max_blocks_per_seq > 0 && !block_tables) return fail(DVATTN_ERR_INVALID, "null block_tables pointer");
+    if ((st = check_aligned({{out, "out", 16}, {queries, "queries", 16}, {k_cache, "k_cache", 16},
+                             {v_cache, "v_cache", 16}, {workspace, "workspace", 16}, {locations, "locations", 4},
+                             {fragment_lengths, "fragment_lengths", 4}, {cosines, "cosines", 4},
+                             {sines, "sines", 4}, {block_tables, "block_tables", 4}})) != DVATTN_OK)
+        return st;
     const size_t need = dvattn_paged_sdpa_workspace_size(dtype, s, -1);
     if (workspace_bytes < need || (need && !workspace))
         return fail(DVATTN_ERR_WORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
@@ -238,6 +266,12 @@ dvattn_status dvattn_varlen_paged_sdpa(int dtype, void* out, float scale, const 
         return fail(DVATTN_ERR_INVALID, "null locations / fragment_lengths / cos / sin pointer");
     if (s->num_blocks > 0 && (!k_cache || !v_cache)) return fail(DVATTN_ERR_INVALID, "null k/v cache pointer");
     if (s->max_blocks_per_seq > 0 && !block_tables) return fail(DVATTN_ERR_INVALID, "null block_tables pointer");
+    if ((st = check_aligned({{out, "out", 16}, {queries, "queries", 16}, {k_cache, "k_cache", 16},
+                             {v_cache, "v_cache", 16}, {workspace, "workspace", 16}, {locations, "locations", 4},
+                             {fragment_lengths, "fragment_lengths", 4}, {cosines, "cosines", 4},
+                             {sines, "sines", 4}, {block_tables, "block_tables", 4},
+                             {cu_seqlens_q, "cu_seqlens_q", 4}})) != DVATTN_OK)
+        return st;
     const size_t need = dvattn_varlen_paged_sdpa_workspace_size(dtype, s, -1);
     if (workspace_bytes < need || (need && !workspace))
         return fail(DVATTN_ERR_WORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
@@ -306,6 +340,10 @@ dvattn_status sdpa_setup(int dtype, void* out, float scale, const int* locations
     if (s->F > 0 && (!locations || !fragment_lengths || !key_fragments || !value_fragments || !fragment_tokens ||
                      !fragment_batch))
         return fail(DVATTN_ERR_INVALID, "null locations / fragment_lengths / fragment arrays");
+    if ((st = check_aligned({{out, "out", 16}, {rotated_queries, "rotated_queries", 16},
+                             {workspace, "workspace", 16}, {locations, "locations", 4},
+                             {fragment_lengths, "fragment_lengths", 4}})) != DVATTN_OK)
+        return st;
     const size_t need = dvattn_sdpa_workspace_size(dtype, s, -1);
     if (workspace_bytes < need || (need && !workspace))
         return fail(DVATTN_ERR_WORKSPACE, "workspace too small: %zu < %zu bytes", workspace_bytes, need);
@@ -448,6 +486,9 @@ dvattn_status rope_setup(int dtype, void* out, const void* queries, const float*
     if ((long long)s->F * s->W * s->Hq * s->S * s->E == 0) return DVATTN_OK;  // rope.cuh:58-60
     if (!out || !queries || (s->rotary_dim > 0 && (!cosines || !sines)))
         return fail(DVATTN_ERR_INVALID, "null pointer");
+    if ((st = check_aligned({{out, "out", elem_bytes(dtype)}, {queries, "queries", elem_bytes(dtype)},
+                             {cosines, "cosines", 4}, {sines, "sines", 4}})) != DVATTN_OK)
+        return st;
     memset(&p, 0, sizeof(p));
     p.out = out;
     p.q = queries;
@@ -509,6 +550,8 @@ dvattn_status dvattn_fused(int dtype, void* out, void* rotated_queries, float sc
     st = sdpa_setup(dtype, out, scale, locations, rotated_queries, fragment_lengths, key_fragments, value_fragments,
                     fragment_tokens, fragment_batch, s, workspace, workspace_bytes, p, tab, max_keys, empty);
     if (st != DVATTN_OK) return st;
+    // the single launch reads the unrotated queries in vectors as well
+    if (!no_rope && (st = check_aligned({{queries, "queries", 16}})) != DVATTN_OK) return st;
     bool refused = false;
     const int chunks = empty || no_rope ? -1 : small_path_chunks(dtype, s, fragment_tokens, true, &refused);
     if (refused) return DVATTN_ERR_UNSUPPORTED;
@@ -551,6 +594,9 @@ dvattn_status dvattn_varlen_rope(int dtype, void* out, const void* queries, cons
     if ((long long)s->F * s->total_q_tokens * s->Hq * s->E == 0) return ok();  // rope.cuh:106-108
     if (!out || !queries || (s->rotary_dim > 0 && (!cosines || !sines)))
         return fail(DVATTN_ERR_INVALID, "null pointer");
+    if ((st = check_aligned({{out, "out", elem_bytes(dtype)}, {queries, "queries", elem_bytes(dtype)},
+                             {cosines, "cosines", 4}, {sines, "sines", 4}})) != DVATTN_OK)
+        return st;
     dv::RopeParams p;
     memset(&p, 0, sizeof(p));
     p.out = out;
@@ -593,6 +639,12 @@ dvattn_status dvattn_paged_kv_append(int dtype, int rope_dtype, void* k_cache, v
     if (!k_cache || !v_cache || !keys || !values || !positions || (s->max_blocks_per_seq > 0 && !block_tables) ||
         (s->rotary_dim > 0 && (!cosines || !sines)))
         return fail(DVATTN_ERR_INVALID, "null pointer");
+    // element-wise copies where the 16-byte vector form does not apply
+    if ((st = check_aligned({{k_cache, "k_cache", elem_bytes(dtype)}, {v_cache, "v_cache", elem_bytes(dtype)},
+                             {keys, "keys", elem_bytes(dtype)}, {values, "values", elem_bytes(dtype)},
+                             {cosines, "cosines", elem_bytes(rope_dtype)}, {sines, "sines", elem_bytes(rope_dtype)},
+                             {positions, "positions", 4}, {block_tables, "block_tables", 4}})) != DVATTN_OK)
+        return st;
     dv::AppendParams p;
     memset(&p, 0, sizeof(p));
     p.kc = k_cache;

@@ -45,6 +45,17 @@
  *   - Keys whose logical page is beyond the block_tables row, or whose page id
  *     is outside [0, num_blocks), are treated as not visible (the reference
  *     reads out of bounds there).
+ *
+ * Alignment (checked; the reference's kernels assumed 16-byte vectors,
+ * paged_kernel_v21.cuh:58-62, without checking): the attention entry points
+ * (dvattn_paged_sdpa[_noalloc], dvattn_varlen_paged_sdpa, dvattn_sdpa,
+ * dvattn_fused) need out, queries, rotated_queries, k_cache, v_cache, every
+ * key/value fragment and the workspace 16-byte aligned and the int32 / fp32
+ * arrays 4-byte aligned; dvattn_rope, dvattn_varlen_rope and
+ * dvattn_paged_kv_append need each array aligned to its element size.  A
+ * pointer off its alignment returns DVATTN_ERR_INVALID, naming the argument.
+ * Tensors from a device allocator, and views of them that start on a row of
+ * the last dimension, always qualify.
  */
 #ifndef DVATTN_AMD_H
 #define DVATTN_AMD_H

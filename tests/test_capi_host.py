@@ -123,6 +123,102 @@ def test_contig_rejects_bad_fragment_batch():
     assert st == 1 and "batch" in L.dvattn_last_error().decode()
 
 
+PAGED_ARGS = ["out", "locations", "queries", "cosines", "sines", "fragment_lengths", "k_cache", "v_cache",
+              "block_tables", "cu_seqlens_q", "workspace"]
+
+
+def _fake_ptrs(names, bad=None, offset=0):
+    """Distinct fake device addresses (never dereferenced: every call below is
+    refused on the host), the one named `bad` moved by `offset` bytes."""
+    return {n: ctypes.c_void_p(0x10000 * (i + 1) + (offset if n == bad else 0)) for i, n in enumerate(names)}
+
+
+def _paged_call(L, a, s, ws_bytes=1 << 30):
+    return L.dvattn_paged_sdpa(2, a["out"], 0.1, a["locations"], a["queries"], a["cosines"], a["sines"],
+                               a["fragment_lengths"], a["k_cache"], a["v_cache"], a["block_tables"],
+                               ctypes.byref(s), a["workspace"], ws_bytes, None)
+
+
+def _varlen_call(L, a, s, ws_bytes=1 << 30):
+    return L.dvattn_varlen_paged_sdpa(2, a["out"], 0.1, a["locations"], a["queries"], a["cosines"], a["sines"],
+                                      a["fragment_lengths"], a["k_cache"], a["v_cache"], a["block_tables"],
+                                      a["cu_seqlens_q"], None, ctypes.byref(s), a["workspace"], ws_bytes, None)
+
+
+# 16-byte vectors / DMAs on the tensors, 4-byte words on the int32 / fp32 arrays
+@pytest.mark.parametrize("name,offset,align", [
+    ("out", 8, 16), ("queries", 2, 16), ("k_cache", 4, 16), ("v_cache", 8, 16), ("workspace", 8, 16),
+    ("locations", 2, 4), ("fragment_lengths", 1, 4), ("cosines", 2, 4), ("sines", 1, 4), ("block_tables", 2, 4),
+])
+def test_paged_and_varlen_refuse_misaligned_pointers(name, offset, align):
+    from dvattention_amd import capi
+    L = capi.lib()
+    s = _shape()
+    a = _fake_ptrs(PAGED_ARGS, name, offset)
+    for call in (_paged_call, _varlen_call):
+        assert call(L, a, s) == 1
+        assert L.dvattn_last_error().decode().startswith(f"{name} must be {align}-byte aligned")
+    a = _fake_ptrs(PAGED_ARGS, "cu_seqlens_q", 2)
+    assert _varlen_call(L, a, s) == 1 and "cu_seqlens_q must be 4-byte" in L.dvattn_last_error().decode()
+    # aligned pointers pass these checks and stop at the (too small) workspace, before any launch
+    a = _fake_ptrs(PAGED_ARGS)
+    assert _paged_call(L, a, s, ws_bytes=16) == 3 and _varlen_call(L, a, s, ws_bytes=16) == 3
+
+
+def test_contig_fused_and_rope_refuse_misaligned_pointers():
+    from dvattention_amd import capi
+    L = capi.lib()
+    s = _shape(W=2, F=1)
+    names = ["out", "rq", "locations", "queries", "fragment_lengths", "cosines", "sines", "workspace", "k", "v"]
+    toks = (ctypes.c_int * 1)(8)
+    batch = (ctypes.c_int * 1)(2)
+
+    def sdpa(a):
+        kp, vp = (ctypes.c_void_p * 1)(a["k"].value), (ctypes.c_void_p * 1)(a["v"].value)
+        return L.dvattn_sdpa(2, a["out"], 0.1, a["locations"], a["rq"], a["fragment_lengths"], kp, vp, toks, batch,
+                             ctypes.byref(s), a["workspace"], 1 << 30, None)
+
+    def fused(a):
+        kp, vp = (ctypes.c_void_p * 1)(a["k"].value), (ctypes.c_void_p * 1)(a["v"].value)
+        return L.dvattn_fused(2, a["out"], a["rq"], 0.1, a["locations"], a["queries"], a["fragment_lengths"], kp, vp,
+                              toks, batch, a["cosines"], a["sines"], ctypes.byref(s), a["workspace"], 1 << 30, None)
+
+    for name, offset, align in [("out", 8, 16), ("rq", 4, 16), ("workspace", 8, 16), ("locations", 2, 4),
+                                ("fragment_lengths", 1, 4)]:
+        for call in (sdpa, fused):
+            assert call(_fake_ptrs(names, name, offset)) == 1
+            assert L.dvattn_last_error().decode().startswith(f"{name.replace('rq', 'rotated_queries')} must be "
+                                                             f"{align}-byte aligned"), (name, call)
+    for name in ("k", "v"):
+        assert sdpa(_fake_ptrs(names, name, 8)) == 1 and "16-byte aligned" in L.dvattn_last_error().decode()
+    # fused: element alignment for the rotation, 16 bytes for the single launch's query reads
+    assert fused(_fake_ptrs(names, "queries", 1)) == 1
+    assert L.dvattn_last_error().decode().startswith("queries must be 2-byte aligned")
+    assert fused(_fake_ptrs(names, "queries", 2)) == 1
+    assert L.dvattn_last_error().decode().startswith("queries must be 16-byte aligned")
+    assert fused(_fake_ptrs(names, "cosines", 2)) == 1 and "cosines must be 4-byte" in L.dvattn_last_error().decode()
+    # standalone rope: natural alignment of the storage type (fp32 4, bf16 2) and of fp32 cos/sin
+    a = _fake_ptrs(names, "out", 2)
+    assert L.dvattn_rope(0, a["out"], a["queries"], a["cosines"], a["sines"], ctypes.byref(s), None) == 1
+    assert L.dvattn_last_error().decode().startswith("out must be 4-byte aligned")
+    a = _fake_ptrs(names, "queries", 1)
+    assert L.dvattn_varlen_rope(2, a["out"], a["queries"], a["cosines"], a["sines"], ctypes.byref(s), None) == 1
+    assert L.dvattn_last_error().decode().startswith("queries must be 2-byte aligned")
+
+
+def test_kv_append_refuses_misaligned_pointers():
+    from dvattention_amd import capi
+    L = capi.lib()
+    s = _kv_shape()
+    lay = capi.KvLayout()
+    names = ["k_cache", "v_cache", "block_tables", "positions", "keys", "values", "cosines", "sines"]
+    for name, offset, rope_dt, align in [("keys", 1, 0, 2), ("v_cache", 1, 0, 2), ("positions", 2, 0, 4),
+                                         ("block_tables", 1, 0, 4), ("cosines", 2, 0, 4), ("sines", 1, 2, 2)]:
+        a = _fake_ptrs(names, name, offset)
+        st = L.dvattn_paged_kv_append(2, rope_dt, *[a[n] for n in names], ctypes.byref(s), ctypes.byref(lay), None)
+        assert st == 1 and L.dvattn_last_error().decode().startswith(f"{name} must be {align}-byte aligned")
+
+
 def test_workspace_query_is_bounded():
     from dvattention_amd import capi
     L = capi.lib()
