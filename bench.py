@@ -2,6 +2,7 @@
 """Benchmark of the MI355X DVAttn operators on the five BASELINE configurations.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--no-cpu]
+    python bench.py --read-ceiling | --mfma-ceiling      (measurement probes only)
 
 One "step" is one call of the operator over one batch of synthetic, seeded
 inputs already resident in HBM.  The headline line (``value``) is configuration
@@ -220,6 +221,49 @@ def plain_read(device, gib: int = 4, calls: int = 10) -> dict:
     return out
 
 
+def mfma_ceiling(device, iters: int = 2000, calls: int = 10) -> dict:
+    """The MFMA rate probe (dv_probe.hip `dvprobe_mfma_rate`): back-to-back
+    v_mfma_f32_16x16x32_bf16 on every SIMD at the chunk kernel's occupancy (eight
+    waves per CU), alone and with n independent fp32 FMAs or v_exp_f32 per MFMA.
+    Per mix: TFLOP/s, the shader clock the waves ran at (s_memtime against the
+    100 MHz s_memrealtime counter), and SIMD cycles per MFMA at that clock."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(HERE, "dvattention_amd", "libdvattn_probe.so"))
+    lib.dvprobe_last_error.restype = ctypes.c_char_p
+    lib.dvprobe_mfma_rate.restype = ctypes.c_int
+    lib.dvprobe_mfma_rate.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_longlong,
+                                      ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    sink = torch.empty(512 * cus, dtype=torch.float32, device=device)
+    clocks = torch.zeros(16 * cus, dtype=torch.int64, device=device)
+    stream = torch.cuda.current_stream()
+    rows = []
+    for n, ex in ((0, 0), (1, 0), (2, 0), (3, 0), (4, 0), (6, 0), (1, 1), (2, 1), (0, 0)):
+        def call():
+            wgs = lib.dvprobe_mfma_rate(n, ex, iters, sink.data_ptr(), sink.numel(), clocks.data_ptr(),
+                                        clocks.numel(), stream.cuda_stream)
+            if wgs < 0:
+                raise RuntimeError(lib.dvprobe_last_error().decode())
+            return wgs
+        for _ in range(2):
+            wgs = call()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(calls):
+            call()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / calls
+        ck = clocks.view(-1, 2).double().sum(0).tolist()
+        mhz = ck[0] / ck[1] * 100.0 if ck[1] > 0 else 0.0
+        mfma_per_simd = iters * 8 * 2                 # two waves per SIMD, eight MFMAs per round
+        rows.append({"other_per_mfma": n, "kind": "exp" if ex else "fma", "us": round(us, 1),
+                     "tflops": round(wgs * 8 * iters * 8 * 16384 / (us * 1e-6) / 1e12, 1),
+                     "clock_mhz": round(mhz), "simd_cycles_per_mfma": round(mhz * us / mfma_per_simd, 2)})
+    return {"cus": cus, "iters": iters, "rows": rows}
+
+
 def _time_calls(fn, n_inputs: int, steps: int, warmup: int) -> tuple:
     """Mean µs per call of fn(j % n_inputs): (a) `steps` eager back-to-back calls
     (HIP events; small kernels are bound by the host's launch rate there) and
@@ -393,6 +437,8 @@ def main() -> int:
     ap.add_argument("--no-cache-rows", action="store_true", help="skip the K-side append / view metadata rows")
     ap.add_argument("--read-ceiling", action="store_true",
                     help="only the paged-read probe on configurations 2 and 4 (one JSON line)")
+    ap.add_argument("--mfma-ceiling", action="store_true",
+                    help="only the MFMA rate probe, alone and with other VALU work per MFMA (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the operator has no multi-GPU path); "
@@ -416,6 +462,13 @@ def main() -> int:
         log(f"[bench] plain streaming read of {plain['bytes'] >> 30} GiB: {plain['nontemporal_GBs']} GB/s "
             f"non-temporal, {plain['default_GBs']} GB/s default policy")
         print(json.dumps({"read_ceiling": rows, "plain_read": plain}), flush=True)
+        return 0
+    if args.mfma_ceiling:
+        res = mfma_ceiling(device)
+        for r in res["rows"]:
+            log(f"[bench] mfma 16x16x32 bf16 + {r['other_per_mfma']} {r['kind']}/MFMA: {r['tflops']} TFLOP/s at "
+                f"{r['clock_mhz']} MHz, {r['simd_cycles_per_mfma']} SIMD cycles per MFMA")
+        print(json.dumps({"mfma_ceiling": res}), flush=True)
         return 0
     cfgs = [int(x) for x in args.configs.split(",") if x]
     if 2 not in cfgs:

@@ -1,4 +1,5 @@
-// Read probes (libdvattn_probe.so, used by `bench.py --read-ceiling`).
+// Measurement probes (libdvattn_probe.so, used by `bench.py --read-ceiling`
+// and `bench.py --mfma-ceiling`).
 //
 // Paged-read probe:
 // the 16-bit decode kernel's K/V stream with the attention taken out.  It runs
@@ -112,6 +113,49 @@ __global__ __launch_bounds__(256) void dv_plain_read(const u32x4* __restrict__ b
         for (int u = 0; u < U; ++u) acc ^= v[u][0] ^ v[u][1] ^ v[u][2] ^ v[u][3];
     }
     if ((threadIdx.x & 63) == 0) sink[blockIdx.x * 4 + (threadIdx.x >> 6)] = acc;
+}
+
+// MFMA rate probe: back-to-back v_mfma_f32_16x16x32_bf16 on every SIMD (eight
+// waves per CU, two per SIMD, as the chunk kernel runs; eight independent
+// accumulator chains per wave) with N other instructions per MFMA, each on an
+// independent register: fp32 FMAs (EXP false) or v_exp_f32 (EXP true).  Every
+// wave records its shader-clock cycles (s_memtime) and 100 MHz reference ticks
+// (s_memrealtime) over the loop, so the host can report the clock it ran at.
+template <int N, bool EXP>
+__global__ __launch_bounds__(512) void dv_mfma_rate(float* sink, unsigned long long* clocks, int iters) {
+    constexpr int kChains = 8;
+    constexpr int kX = N > 0 ? N : 1;
+    const int lane = threadIdx.x & 63;
+    const u32x4 a = {0x3f803f80u ^ (unsigned)lane, 0x3f003f00u, 0x3e803e80u + (unsigned)lane, 0x3f803f00u};
+    const u32x4 b = {0x3f003f80u, 0x3e803f80u ^ (unsigned)(lane << 3), 0x3f803f80u, 0x3f003f00u};
+    f32x4 c[kChains];
+#pragma unroll
+    for (int i = 0; i < kChains; ++i) c[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float x[kX];
+#pragma unroll
+    for (int v = 0; v < kX; ++v) x[v] = (float)(lane + v) * 0.01f;
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < kChains; ++i) {
+            c[i] = Tr<kBF16>::mma(a, b, c[i]);
+#pragma unroll
+            for (int v = 0; v < N; ++v)
+                x[v] = EXP ? __builtin_amdgcn_exp2f(x[v]) : __builtin_fmaf(x[v], 0.999f, 0.5f);
+        }
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.f;
+#pragma unroll
+    for (int v = 0; v < kX; ++v) s += x[v];
+#pragma unroll
+    for (int i = 0; i < kChains; ++i) s += c[i][0] + c[i][1] + c[i][2] + c[i][3];
+    sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+    const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (lane == 0) {
+        clocks[2 * w] = t1 - t0;
+        clocks[2 * w + 1] = r1 - r0;
+    }
 }
 
 thread_local const char* g_msg = "";
@@ -237,6 +281,54 @@ __attribute__((visibility("default"))) int dvprobe_plain_read(const void* buf, s
     }
     g_msg = "";
     return 0;
+}
+
+// MFMA 16x16x32 bf16 rate with `n_other` independent fp32 FMAs (exp = 0) or
+// v_exp_f32 (exp = 1) per MFMA: one workgroup of eight waves per CU, `iters`
+// rounds of eight MFMAs per wave.  n_other is 0, 1, 2, 3, 4 or 6 for FMAs and
+// 1 or 2 for exponentials.  `sink` takes 512 floats per CU; `clocks` two words
+// per wave (shader cycles, 100 MHz ticks; 16 per CU).  Returns the number of
+// workgroups launched, or -1 with a message for dvprobe_last_error().
+__attribute__((visibility("default"))) int dvprobe_mfma_rate(int n_other, int exp, int iters, float* sink,
+                                                              long long sink_floats, unsigned long long* clocks,
+                                                              long long clock_words, void* stream) {
+    using namespace dv;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        g_msg = "probe: no device";
+        return -1;
+    }
+    const int cus = device_cu_count(device);
+    if (!sink || !clocks || iters <= 0 || sink_floats < 512ll * cus || clock_words < 16ll * cus) {
+        g_msg = "probe: mfma rate needs iters > 0, 512 sink floats and 16 clock words per CU";
+        return -1;
+    }
+    void (*k)(float*, unsigned long long*, int) = nullptr;
+    if (!exp) {
+        switch (n_other) {
+            case 0: k = dv_mfma_rate<0, false>; break;
+            case 1: k = dv_mfma_rate<1, false>; break;
+            case 2: k = dv_mfma_rate<2, false>; break;
+            case 3: k = dv_mfma_rate<3, false>; break;
+            case 4: k = dv_mfma_rate<4, false>; break;
+            case 6: k = dv_mfma_rate<6, false>; break;
+            default: break;
+        }
+    } else {
+        if (n_other == 1) k = dv_mfma_rate<1, true>;
+        if (n_other == 2) k = dv_mfma_rate<2, true>;
+    }
+    if (!k) {
+        g_msg = "probe: unsupported mix (FMAs: 0, 1, 2, 3, 4, 6; exponentials: 1, 2)";
+        return -1;
+    }
+    hipLaunchKernelGGL(k, dim3(cus), dim3(512), 0, (hipStream_t)stream, sink, clocks, iters);
+    if (hipGetLastError() != hipSuccess) {
+        g_msg = "probe: launch failed";
+        return -1;
+    }
+    g_msg = "";
+    return cus;
 }
 
 }  // extern "C"
