@@ -289,6 +289,38 @@ def test_paged_empty_rows_zero_and_noop(dv, gpu):
                                          g["block_tables"])
 
 
+def test_misaligned_views_are_refused(dv, gpu):
+    """A contiguous view whose start breaks the 16-byte alignment of the kernels'
+    vector loads is refused on the host with the argument named (RuntimeError
+    through the torch op), never launched; the same data aligned runs."""
+    d = to(rand_paged(1, 2, 1, 1, 16, [40], 64, torch.bfloat16, seed=11), gpu)
+
+    def shifted(t, elems):
+        flat = torch.empty(t.numel() + elems, dtype=t.dtype, device=gpu)
+        v = flat[elems:].view(t.shape)
+        v.copy_(t)
+        return v
+
+    def call(q, kc):
+        out = torch.zeros(q.shape, dtype=q.dtype, device=gpu)
+        torch.ops.libdvatt.dvattn_paged_sdpa(out, 0.1, d["locations"], q, d["cosines"], d["sines"],
+                                             d["fragment_lengths"], kc, d["v_cache"], d["block_tables"])
+        return out
+
+    qm = shifted(d["queries"], 1)             # 2 bytes past a 16-byte boundary
+    assert qm.is_contiguous() and qm.data_ptr() % 16 == 2
+    with pytest.raises(RuntimeError, match="queries must be 16-byte aligned"):
+        call(qm, d["k_cache"])
+    km = shifted(d["k_cache"], 4)             # 8 bytes off
+    with pytest.raises(RuntimeError, match="k_cache must be 16-byte aligned"):
+        call(d["queries"], km)
+    # aligned views of the same data (16-byte offsets) run and agree
+    ref = call(d["queries"], d["k_cache"])
+    got = call(shifted(d["queries"], 8), shifted(d["k_cache"], 8))
+    assert torch.equal(got, ref) and torch.count_nonzero(ref) > 0
+    torch.cuda.synchronize()
+
+
 def test_paged_invalid_pages_are_masked(dv, gpu):
     # a block_tables entry outside the page pool hides its keys (no out-of-bounds read)
     d = rand_paged(1, 2, 1, 1, 16, [64], 64, torch.float32, seed=7, loc=np.array([[[63], [63]]]))
