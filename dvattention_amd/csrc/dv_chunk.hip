@@ -139,16 +139,10 @@ __device__ inline void issue_stage(const DecodeParams& p, const Range& r, const 
 struct Tile {
     f32x4 o[8];
     float m, l;
+    // -max(m, -FLT_MAX), the exponent offset of every stage: kept beside m and
+    // updated only where m changes (sm_raise), not recomputed per stage
+    float nm;
 };
-
-// Online softmax of one tile for one 32-key stage (softmax32); returns the P^T
-// MFMA operand.
-template <int DT>
-__device__ inline POperand tile_softmax(Tile& t, const f32x4& s0, const f32x4& s1, uint32_t mask, float l2scale) {
-    float pr[8];
-    softmax32<false>(t.o, t.m, t.l, s0, s1, mask, l2scale, pr);
-    return p_operands<DT>(pr, t.l);
-}
 
 // Query tiles of this wave's tokens for view f, staged through LDS (the K/V ring
 // is idle between view ranges): raw q rows arrive by direct-to-LDS loads, each
@@ -387,16 +381,19 @@ __device__ inline uint32_t token_mask(int vis, int kb0) {
 // exponents.  Part 2 (sm_finish): the probabilities, the row sums and the P^T
 // operands.  Same arithmetic as softmax32 + p_operands.
 __device__ inline float sm_exponents(const Tile& t, const f32x4& s0, const f32x4& s1, float l2, float (&pr)[8]) {
-    // a row with no max yet (m = -inf) subtracts -FLT_MAX instead: a visible
-    // key's exponent is then huge (the row takes sm_raise) and an invisible
-    // key's stays -inf, where -inf - (-inf) would be NaN
-    const float nm = -fmaxf(t.m, -3.402823466e38f);
+    // a row with no max yet (m = -inf) subtracts -FLT_MAX instead (t.nm): a
+    // visible key's exponent is then huge (the row takes sm_raise) and an
+    // invisible key's stays -inf, where -inf - (-inf) would be NaN
+    const float nm = t.nm;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         pr[i] = __builtin_fmaf(s0[i], l2, nm);
         pr[4 + i] = __builtin_fmaf(s1[i], l2, nm);
     }
-    return fmaxf(fmaxf(fmaxf(pr[0], pr[1]), fmaxf(pr[2], pr[3])), fmaxf(fmaxf(pr[4], pr[5]), fmaxf(pr[6], pr[7])));
+    // shaped for three-operand maxima: max3(max3(0,1,2), max3(3,4,5), max(6,7)),
+    // four instructions where a balanced pairwise tree compiled to five
+    const float a = fmaxf(fmaxf(pr[0], pr[1]), pr[2]), b = fmaxf(fmaxf(pr[3], pr[4]), pr[5]);
+    return fmaxf(fmaxf(a, b), fmaxf(pr[6], pr[7]));
 }
 
 __device__ inline void sm_raise(Tile& t, const f32x4& s0, const f32x4& s1, float l2, float (&pr)[8]) {
@@ -415,6 +412,7 @@ __device__ inline void sm_raise(Tile& t, const f32x4& s0, const f32x4& s1, float
 #pragma unroll
         for (int c = 0; c < 8; ++c) t.o[c] *= alpha;
         t.m = mnew;
+        t.nm = -fmaxf(mnew, -3.402823466e38f);
     }
     const float mm = t.m == -DV_INF ? 0.0f : t.m;  // p = 0 while the row has no visible key
 #pragma unroll
@@ -430,8 +428,14 @@ __device__ inline POperand sm_finish(Tile& t, float (&pr)[8]) {
 
 // Register tie: the values are complete at this point in program order (the
 // compiler may not move their computation past it, e.g. across a workgroup
-// barrier into the next half-stage).
-__device__ inline void settle(POperand& a) { asm volatile("" : "+v"(a.hi), "+v"(a.lo)); }
+// barrier into the next half-stage).  Only the words the P V MFMAs read are
+// tied: bf16 has no residual operand, and tying its (zero) lo made the
+// compiler rebuild and copy four zero registers every half-stage.
+template <int DT>
+__device__ inline void settle(POperand& a) {
+    asm volatile("" : "+v"(a.hi));
+    if constexpr (DT == kF16) asm volatile("" : "+v"(a.lo));
+}
 
 // Keys [sa, sbnd) of the current view for this wave's two tiles (A = tile 0,
 // B = tile 1): the stage loop.  Ring slot i % kStages holds stage i.  Per
@@ -502,7 +506,7 @@ __device__ inline void stream_range(const DecodeParams& p, const Range& r, const
             __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS read
             __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
         }
-        settle(pa);
+        settle<DT>(pa);
         lds_wait();
         wait_vmcnt<kDmaPerStage * (kAhead - 2)>();  // own share of stage i + 1 landed
         wg_barrier();
@@ -530,7 +534,7 @@ __device__ inline void stream_range(const DecodeParams& p, const Range& r, const
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
             __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);  // VALU
         }
-        settle(pb);
+        settle<DT>(pb);
     }
     // P V of B's last stage
     mfma_settle(tl[1].o);
@@ -559,6 +563,7 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
         for (int c = 0; c < 8; ++c) tl[t].o[c] = f32x4{0.f, 0.f, 0.f, 0.f};
         tl[t].m = -DV_INF;
         tl[t].l = 0.0f;
+        tl[t].nm = 3.402823466e38f;
     }
 
     long long P = 0, off = 0;
