@@ -5,7 +5,7 @@ block sizes, KV heads, query tokens per sequence (S = 1 takes the decode
 kernels, S >= 2 the multi-query kernel for 16-bit types) and dtypes.  Each case
 is small enough for the oracle to finish in well under a second.
 
-DVATTN_RANDOM_CASES (default 40) and DVATTN_RANDOM_SEED0 (default 0) widen or
+DVATTN_RANDOM_CASES (default 200) and DVATTN_RANDOM_SEED0 (default 0) widen or
 move the sweep; the default run is the one the suite commits to.
 """
 import os
@@ -20,7 +20,7 @@ from test_gpu_parity import close, hf_cs, rand_paged, rand_varlen, run_paged, ru
 pytestmark = pytest.mark.gpu
 
 DT = [torch.float32, torch.float16, torch.bfloat16]
-CASES = int(os.environ.get("DVATTN_RANDOM_CASES", "40"))
+CASES = int(os.environ.get("DVATTN_RANDOM_CASES", "200"))
 SEED0 = int(os.environ.get("DVATTN_RANDOM_SEED0", "0"))
 
 
