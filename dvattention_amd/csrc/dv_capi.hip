@@ -388,6 +388,21 @@ dvattn_status sdpa_setup(int dtype, void* out, float scale, const int* locations
     return DVATTN_OK;
 }
 
+// View descriptors written into the device view table by a kernel whose
+// arguments carry them: the values travel with the launch (a captured graph
+// keeps its own copy), so no host buffer has to outlive the call, as a
+// host-to-device copy from the caller's memory would in a captured graph.
+constexpr int kFragFillBatch = 64;  // descriptors per launch: 2 KiB of kernel arguments
+struct FragFill {
+    dv::FragDesc d[kFragFillBatch];
+    int first, n;
+};
+
+__global__ __launch_bounds__(kFragFillBatch) void dv_frag_fill(dv::FragDesc* dst, const FragFill b) {
+    const int i = threadIdx.x;
+    if (i < b.n) dst[b.first + i] = b.d[i];
+}
+
 // The general contiguous-view launch: view table (F > kMaxFragArgs) to the
 // workspace, then the decode or chunk kernel on already-rotated queries.
 dvattn_status sdpa_launch(int dtype, dv::DecodeParams& p, const std::vector<dv::FragDesc>& tab, long long max_keys,
@@ -396,10 +411,18 @@ dvattn_status sdpa_launch(int dtype, dv::DecodeParams& p, const std::vector<dv::
     size_t ws_left = workspace_bytes;
     const size_t tab_bytes = contig_table_bytes(p.F);
     if (tab_bytes) {
-        hipError_t e =
-            hipMemcpyAsync(workspace, tab.data(), (size_t)p.F * sizeof(dv::FragDesc), hipMemcpyHostToDevice, stream);
-        if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa fragment table upload");
-        p.frag_tab = reinterpret_cast<const dv::FragDesc*>(workspace);
+        dv::FragDesc* dst = reinterpret_cast<dv::FragDesc*>(workspace);
+        for (int first = 0; first < p.F; first += kFragFillBatch) {
+            FragFill b;
+            memset(&b, 0, sizeof(b));
+            b.first = first;
+            b.n = p.F - first < kFragFillBatch ? p.F - first : kFragFillBatch;
+            for (int i = 0; i < b.n; ++i) b.d[i] = tab[(size_t)(first + i)];
+            hipLaunchKernelGGL(dv_frag_fill, dim3(1), dim3(kFragFillBatch), 0, stream, dst, b);
+            const hipError_t e = hipGetLastError();
+            if (e != hipSuccess) return hip_fail(e, "dvattn_sdpa view table");
+        }
+        p.frag_tab = dst;
         ws = reinterpret_cast<unsigned char*>(workspace) + tab_bytes;
         ws_left -= tab_bytes;
     }
@@ -415,14 +438,16 @@ dvattn_status sdpa_launch(int dtype, dv::DecodeParams& p, const std::vector<dv::
     return ok();
 }
 
-// Whether the single-launch path takes a validated contiguous-view call: fp32,
-// at most kMaxFragArgs views of at most kSmallMaxChunks chunks together, and
-// its partials within the documented workspace size of the shape (so the
-// choice depends on the shape and the fragment lengths only); rotating calls
-// (dvattn_fused) also need rotary_dim % 8 == 0.  Returns the chunk count, or -1
-// for the general path.
-// DVATTN_SMALL_PATH (read on every call): "0" turns the path off; "require"
-// makes a call it cannot take fail with DVATTN_ERR_UNSUPPORTED (*refused).
+// Whether the single-launch path takes a validated contiguous-view call (fp32,
+// fp16 or bf16): at most kMaxFragArgs views of at most kSmallMaxChunks chunks
+// together, and its partials within the documented workspace size of the shape
+// (so the choice depends on the shape and the fragment lengths only); rotating
+// calls (dvattn_fused) also need rotary_dim % 8 == 0.  Returns the chunk count,
+// or -1 for the general path.
+// DVATTN_SMALL_PATH (read with getenv on every call): "0" turns the path off;
+// "require" makes a call it cannot take fail with DVATTN_ERR_UNSUPPORTED
+// (*refused).  Changing the variable while other threads call into the library
+// is undefined (getenv races with setenv); set it before the first call.
 int small_path_chunks(int dtype, const dvattn_shape* s, const int* fragment_tokens, bool rotating, bool* refused) {
     *refused = false;
     const char* env = getenv("DVATTN_SMALL_PATH");
@@ -432,12 +457,14 @@ int small_path_chunks(int dtype, const dvattn_shape* s, const int* fragment_toke
     if (s->F >= 1 && s->F <= dv::kMaxFragArgs && (!rotating || s->rotary_dim % 8 == 0)) {
         chunks = dv::small_chunks(s->F, fragment_tokens);
         const long long items = (long long)s->W * s->S * s->Hkv;
-        // Views of one chunk each need no merge.  Otherwise every workgroup
-        // pays the merge protocol's fences, whose cost grows with the number of
-        // workgroups: past items x chunks = small_max_merged() the general path
-        // (rotation, decode and merge launches) is faster (measured crossover
-        // about 190 workgroups for fp32, about 110 for 16-bit types, whose
-        // general path is faster).
+        // Only a single-chunk call (one view of at most kSmallChunk keys) needs
+        // no merge.  Any other call (several chunks, from one long view or
+        // from several views) merges its chunks in the launch, and every
+        // workgroup pays the merge protocol's fences, whose cost grows with the
+        // number of workgroups: past items x chunks = small_max_merged() the
+        // general path (rotation, decode and merge launches) is faster
+        // (measured crossover about 190 workgroups for fp32, about 110 for
+        // 16-bit types, whose general path is faster).
         if (chunks > 1 && items * chunks > dv::small_max_merged(dtype)) chunks = -1;
         if (chunks >= 1 && dv::small_workspace_bytes(items, chunks) > dvattn_sdpa_workspace_size(dtype, s, -1))
             chunks = -1;

@@ -33,9 +33,9 @@
 //    invalidate the L2 of the workgroup's XCD, work that grows with the
 //    number of workgroups in flight (measured: +2-3 us at 64 workgroups of
 //    several chunks, +18 us at 256).  The host therefore sends a call here
-//    only when its views fit one chunk each (no merge, no fence) or when
-//    items x chunks is small (dv_capi.hip: small_path_chunks); larger calls
-//    take the general path.
+//    only when it has a single chunk per item (one view of at most
+//    kSmallChunk keys: no merge, no fence) or when items x chunks is small
+//    (dv_capi.hip: small_path_chunks); larger calls take the general path.
 #include <string.h>
 
 #include <atomic>

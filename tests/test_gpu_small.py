@@ -8,10 +8,11 @@ to exercise it.  Outputs are checked against the CPU oracle (tolerances 1e-5
 fp32, 1e-3 fp16, 2e-2 bf16, as in test_gpu_parity) and against the general
 path (DVATTN_SMALL_PATH=0) on the same inputs; rotated queries bit-exactly
 against the oracle's rotation (fp32 math rounded to the storage type).
-A call whose rows have more than one chunk takes the single launch only up
-to 160 (fp32) or 96 (16-bit) workgroups (rows x KV heads x chunks): past that
-the call must be refused under require; views of one chunk each have no such
-limit.  The chunk merge
+A call whose rows have more than one chunk (one long view, or several
+views) takes the single launch only up to 160 (fp32) or 96 (16-bit)
+workgroups (rows x KV heads x chunks): past that the call must be refused
+under require; only a single-chunk call (one view of at most 64 keys) has no
+such limit.  The chunk merge
 is exercised from one chunk (direct output) to the 64-chunk maximum, with
 empty views, views past every location, batch-1 views, fragment lengths
 below the tensor length and several query tokens per sequence.  The arrival
@@ -198,4 +199,45 @@ def test_small_graph_replays(dv, gpu, require_small, dtype):
         assert torch.equal(out, eager), f"replay {i}"
         run_fused(dv, e, gpu)
         torch.cuda.synchronize()
+    del graph
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_many_views_graph_replays(dv, gpu, dtype):
+    # more views than kernel arguments hold (20 > 16) take the general path,
+    # whose view table is written on the device by a launch that carries the
+    # descriptors: a captured call must replay correctly after the host-side
+    # arrays of the capturing call are gone
+    F = 20
+    d = make_case(F, 2, 1, 1, [5 + 7 * i for i in range(F)], [2] * F, seed=21, dtype=dtype)
+    e = make_case(F, 2, 1, 1, [9 + 3 * i for i in range(F)], [2] * F, seed=22, dtype=dtype)
+    q, loc, fl, c, s = (d[k].to(gpu) for k in ("q", "loc", "fl", "c", "s"))
+    gk, gv = [k.to(gpu) for k in d["keys"]], [v.to(gpu) for v in d["vals"]]
+    rq = torch.empty(F, 2, 16, 1, 128, dtype=dtype, device=gpu)
+    out = torch.empty(2, 16, 1, 128, dtype=dtype, device=gpu)
+
+    def call():
+        dv.dvattn_fused(q, loc, gk, gv, 0.1, fl, c, s, rotated_queries=rq, out=out)
+
+    call()
+    torch.cuda.synchronize()
+    eager = out.clone()
+    ref = O.fused(0.1, d["loc"], d["q"], d["fl"], d["keys"], d["vals"], d["c"], d["s"])[0]
+    close(eager, ref, dtype, "20 views eager")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        call()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        call()
+    for i in range(4):
+        run_fused(dv, e, gpu)  # eager calls of another 20-view shape between replays
+        torch.cuda.synchronize()
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
     del graph

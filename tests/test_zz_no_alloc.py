@@ -2,8 +2,11 @@
 dvattn_paged_sdpa with a caller workspace, through the C ABI: two calls in a
 row, the second with a smaller input, bit-identical to the workspace entry
 point and within the parity tolerance of the oracle; the decode (S = 1) and
-the multi-query (S >= 2) kernels; and a shape whose scratch need exceeds the
-static array rejected before anything runs.
+the multi-query (S >= 2) kernels; a shape whose scratch need exceeds the
+static array rejected before anything runs; and, for the callers the entry
+point is for, repeated calls that leave the device's free memory unchanged
+and a captured graph whose replays (with eager calls on the same scratch
+between them) equal the eager result.
 """
 import ctypes
 
@@ -64,3 +67,51 @@ def test_noalloc_rejects_oversize(gpu):
     assert ei.value.status == 3 and "scratch" in str(ei.value)
     torch.cuda.synchronize()
     assert torch.count_nonzero(out) == 0
+
+
+@pytest.mark.parametrize("S", [1, 16])
+def test_noalloc_allocates_nothing_and_replays(gpu, S):
+    from dvattention_amd import capi
+    print(f"noalloc graph: S={S}", flush=True)
+    d = rand_paged(2, 6, S, 8, 16, [900, 1400], 128, torch.bfloat16, seed=31)
+    e = to(rand_paged(1, 3, 1, 4, 16, [500], 64, torch.bfloat16, seed=32), gpu)
+    g = to(d, gpu)
+    out = torch.empty(6, 128, S, 128, dtype=torch.bfloat16, device=gpu)
+    other = torch.empty(3, 64, 1, 128, dtype=torch.bfloat16, device=gpu)
+    args = (0.09, g["locations"], g["queries"], g["cosines"], g["sines"], g["fragment_lengths"], g["k_cache"],
+            g["v_cache"], g["block_tables"])
+    eargs = (0.07, e["locations"], e["queries"], e["cosines"], e["sines"], e["fragment_lengths"], e["k_cache"],
+             e["v_cache"], e["block_tables"])
+    capi.paged_sdpa_noalloc(out, *args)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    close(eager, O.paged_sdpa(0.09, **d), torch.bfloat16, "noalloc eager")
+    # nothing allocated: the device's free memory is the same after more calls
+    free0 = torch.cuda.mem_get_info(gpu)[0]
+    for _ in range(3):
+        capi.paged_sdpa_noalloc(out, *args)
+        capi.paged_sdpa_noalloc(other, *eargs)
+    torch.cuda.synchronize()
+    assert torch.cuda.mem_get_info(gpu)[0] == free0
+    # captured, then replayed with eager calls on the shared scratch between
+    stream = torch.cuda.Stream(gpu)
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        capi.paged_sdpa_noalloc(out, *args)
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        capi.paged_sdpa_noalloc(out, *args)
+    eref = None
+    for i in range(4):
+        capi.paged_sdpa_noalloc(other, *eargs)
+        torch.cuda.synchronize()
+        if eref is None:
+            eref = other.clone()
+        assert torch.equal(other, eref), f"eager call {i} between replays"
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+    del graph
