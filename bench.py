@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X DVAttn operators on the five BASELINE configurations.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,5v] [--no-cpu]
     python bench.py --read-ceiling | --mfma-ceiling      (measurement probes only)
 
 One "step" is one call of the operator over one batch of synthetic, seeded
@@ -11,7 +11,8 @@ steps are timed back to back between two synchronisations; ``value`` is the
 achieved algorithmic HBM rate in TB/s and ``ms_per_step`` the time per call.
 Inputs rotate over enough replicas that consecutive calls never find their K/V
 in the 256 MB Infinity Cache (cold HBM reads, as in a real multi-layer decode
-step).  Every configuration is also reported under ``per_config``, and the
+step).  Every configuration is also reported under ``per_config`` (``5v``:
+configuration 5's 16-token chunks packed through the varlen op, its cross-check), and the
 cache-side kernels around the path (K-side append, merge_caches re-rotation,
 view metadata) under ``cache_rows``.
 
@@ -59,14 +60,14 @@ def replicas_for(wl_bytes: int, max_replicas: int = 4096) -> int:
 MIN_TIMED_US = 2000.0
 
 
-def time_config(i: int, steps: int, warmup: int, device, exact: bool = False) -> dict:
-    """Per-call time of configuration i.  exact: time exactly `steps` calls (the
-    headline); otherwise at least `steps` calls and at least MIN_TIMED_US of
-    work, estimated from the warm-up calls."""
+def time_config(i, steps: int, warmup: int, device, exact: bool = False) -> dict:
+    """Per-call time of configuration i (1-5 or "5v").  exact: time exactly
+    `steps` calls (the headline); otherwise at least `steps` calls and at least
+    MIN_TIMED_US of work, estimated from the warm-up calls."""
     from dvattention_amd import workloads as WL
-    first = WL.config(i, device=device, seed=1234)
+    first = WL.workload(i, device=device, seed=1234)
     R = replicas_for(first.meta.get("kv_bytes", first.alg_bytes))
-    wls = [first] + [WL.config(i, device=device, seed=1234 + r) for r in range(1, R)]
+    wls = [first] + [WL.workload(i, device=device, seed=1234 + r) for r in range(1, R)]
     outs = [w.out_like() for w in wls]
     rqs = [torch.empty(w.meta["rq_shape"], dtype=w.dtype, device=device) if w.op == "fused" else None for w in wls]
     for j in range(warmup):
@@ -432,7 +433,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="1,2,3,4,5")
+    ap.add_argument("--configs", default="1,2,3,4,5,5v")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-cache-rows", action="store_true", help="skip the K-side append / view metadata rows")
     ap.add_argument("--read-ceiling", action="store_true",
@@ -470,7 +471,7 @@ def main() -> int:
                 f"{r['clock_mhz']} MHz, {r['simd_cycles_per_mfma']} SIMD cycles per MFMA")
         print(json.dumps({"mfma_ceiling": res}), flush=True)
         return 0
-    cfgs = [int(x) for x in args.configs.split(",") if x]
+    cfgs = [x if x == "5v" else int(x) for x in args.configs.split(",") if x]
     if 2 not in cfgs:
         cfgs = [2] + cfgs
     per = {}
@@ -521,7 +522,7 @@ def main() -> int:
                      "launch_us": head["kernel_us_mean"], "copy_GBs": round(copy_gbs, 1),
                      "read_ceiling": ceiling},
         "cpu_baseline": cpu,
-        "per_config": [per[i] for i in sorted(per)],
+        "per_config": [per[i] for i in sorted(per, key=str)],
         "cache_rows": cache_rows,
     }
     print(json.dumps(line), flush=True)

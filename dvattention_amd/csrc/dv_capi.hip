@@ -242,6 +242,8 @@ dvattn_status dvattn_paged_sdpa_noalloc(int dtype, void* out, float scale, const
 // ---------------------------------------------------------------------------
 size_t dvattn_varlen_paged_sdpa_workspace_size(int dtype, const dvattn_shape* s, int device) {
     if (!s || !valid_dtype(dtype)) return 0;
+    if (dv::use_varlen_chunk(dtype, s->total_q_tokens, s->W))
+        return dv::varlen_chunk_workspace_bytes(s->total_q_tokens, s->W, s->Hkv, current_device(device));
     return dv::decode_workspace_bytes(s->total_q_tokens, s->Hkv, current_device(device), dtype);
 }
 
@@ -302,8 +304,17 @@ dvattn_status dvattn_varlen_paged_sdpa(int dtype, void* out, float scale, const 
     p.nblocks = s->num_blocks;
     p.min_keys = dv::kDecodeMinKeys;
     const long long max_keys = (long long)s->max_blocks_per_seq * s->block_size;
-    hipError_t e = dv::launch_decode(dtype, dv::kQRotHalf, dv::kKvPaged, dv::kRowVarlen, p, s->total_q_tokens,
-                                     max_keys, workspace, workspace_bytes, (hipStream_t)stream);
+    hipError_t e;
+    if (dv::use_varlen_chunk(dtype, s->total_q_tokens, s->W)) {
+        // two or more packed tokens per sequence on average: each sequence's
+        // tokens share one K/V stream (the reference re-reads K/V per token,
+        // varlen_paged_kernel_v21.cuh:388)
+        p.min_keys = 256;
+        e = dv::launch_varlen_chunk(dtype, p, max_keys, workspace, workspace_bytes, (hipStream_t)stream);
+    } else {
+        e = dv::launch_decode(dtype, dv::kQRotHalf, dv::kKvPaged, dv::kRowVarlen, p, s->total_q_tokens, max_keys,
+                              workspace, workspace_bytes, (hipStream_t)stream);
+    }
     if (e != hipSuccess) return hip_fail(e, "dvattn_varlen_paged_sdpa launch");
     return ok();
 }

@@ -27,6 +27,8 @@
 //  * Rows are causal-masked per token (key l visible iff l <= locations[f,w,s]).
 //  * The balanced split / LSE merge is the decode kernel's (equal key chunks per
 //    workgroup, fp32 partial slots, dv_merge_chunk).
+#include <climits>
+
 #include "dv_common.h"
 #include "dv_device.h"
 #include "dv_schedule.h"
@@ -144,37 +146,85 @@ struct Tile {
     float nm;
 };
 
-// Query tiles of this wave's tokens for view f, staged through LDS (the K/V ring
-// is idle between view ranges): raw q rows arrive by direct-to-LDS loads, each
-// lane rotates whole (d, d + R/2) pairs in place (src/rope.cuh:18-51: first R/2
-// cos/sin entries, separately rounded fp32 products and sum, rounded to the
-// storage type; dims >= R untouched), then lane (g, n) reads
-// Q[n][c*32 + g*8 + 0..7] of every tile.  Wave-private LDS region: 8 KiB.
-template <int DT, int QM>
-__device__ inline void stage_q_tiles(const DecodeParams& p, unsigned char* qreg, float* csreg, int w, int tok0,
-                                     int ntile, int f, int hkv, u32x4 (&qB)[kTiles][4]) {
+// A row group: up to kTokBlk query tokens of one sequence that share one K/V
+// stream.  kRowWS: group rg is block rg % nsb of sequence rg / nsb in the
+// [W, S] token grid (tokens s0 .. s0 + ntok - 1); kRowVarlen: entry rg of the
+// table dv_varlen_groups writes (packed tokens lin .. lin + ntok - 1 of
+// sequence w).  lin: the first token's index on the token axis of locations
+// and cos/sin (w * S + s0, or the packed token).
+struct Grp {
+    int w, s0, lin, ntok;
+};
+
+template <int RM>
+__device__ inline Grp group_of(const DecodeParams& p, int rg) {
+    Grp g;
+    if (RM == kRowVarlen) {
+        const int4 e = reinterpret_cast<const int4*>(p.vgroups)[rg];
+        g.lin = e.x;
+        g.ntok = e.y;
+        g.w = e.z;
+        g.s0 = 0;
+    } else {
+        const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
+        g.w = rg / nsb;
+        g.s0 = (rg - g.w * nsb) * kTokBlk;
+        g.ntok = p.S - g.s0 < kTokBlk ? p.S - g.s0 : kTokBlk;
+        g.lin = g.w * p.S + g.s0;
+    }
+    return g;
+}
+
+// Length of the token axis of locations [F, tokens] and cos/sin.
+template <int RM>
+__device__ inline long long tok_axis(const DecodeParams& p) {
+    return RM == kRowVarlen ? (long long)p.T : (long long)p.W * p.S;
+}
+
+// Element offset of the query row (head h) and of the output row of token i
+// of group g (view f for pre-rotated queries [F, W, Hq, S, E]).
+template <int QM, int RM>
+__device__ inline long long q_row(const DecodeParams& p, const Grp& g, int i, int h, int f) {
+    if (RM == kRowVarlen) return ((long long)(g.lin + i) * p.Hq + h) * kHeadDim;
+    if (QM == kQPre) return ((((long long)f * p.W + g.w) * p.Hq + h) * p.S + g.s0 + i) * kHeadDim;
+    return (((long long)g.w * p.Hq + h) * p.S + g.s0 + i) * kHeadDim;
+}
+template <int RM>
+__device__ inline long long out_row(const DecodeParams& p, const Grp& g, int i, int h) {
+    if (RM == kRowVarlen) return ((long long)(g.lin + i) * p.Hq + h) * kHeadDim;
+    return (((long long)g.w * p.Hq + h) * p.S + g.s0 + i) * kHeadDim;
+}
+
+// Query tiles of this wave's tokens tok0 .. tok0 + ntile - 1 of group gr for
+// view f, staged through LDS (the K/V ring is idle between view ranges): raw
+// q rows arrive by direct-to-LDS loads, each lane rotates whole (d, d + R/2)
+// pairs in place (src/rope.cuh:18-51 and :67-114: first R/2 cos/sin entries of
+// the token's full-width row, or its half-width varlen row; separately rounded
+// fp32 products and sum, rounded to the storage type; dims >= R untouched),
+// then lane (g, n) reads Q[n][c*32 + g*8 + 0..7] of every tile.  Wave-private
+// LDS region: 8 KiB.
+template <int DT, int QM, int RM>
+__device__ inline void stage_q_tiles(const DecodeParams& p, unsigned char* qreg, float* csreg, const Grp& gr,
+                                     int tok0, int ntile, int f, int hkv, u32x4 (&qB)[kTiles][4]) {
 #pragma clang fp contract(off)
     using raw = typename Tr<DT>::raw;
     const int lane = opaque_tid() & 63;
     const int g = lane >> 4, n = lane & 15;
     const uint32_t qbase = lds_addr(qreg);
     for (int t = 0; t < ntile; ++t) {
-        const int s = tok0 + t;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const int hn = i * 4 + (lane >> 4);
             const int h = hkv * kGqa + hn;
-            const raw* q = QM == kQPre
-                               ? reinterpret_cast<const raw*>(p.q) +
-                                     ((((long long)f * p.W + w) * p.Hq + h) * p.S + s) * kHeadDim
-                               : reinterpret_cast<const raw*>(p.q) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+            const raw* q = reinterpret_cast<const raw*>(p.q) + q_row<QM, RM>(p, gr, tok0 + t, h, f);
             dma16(q + (lane & 15) * 8, __builtin_amdgcn_readfirstlane(qbase + (uint32_t)(t * 4096 + i * 1024)));
         }
     }
     const int half = p.R >> 1;
     if (QM != kQPre) {
         for (int t = 0; t < ntile; ++t) {
-            const long long co = (((long long)f * p.W + w) * p.S + tok0 + t) * p.R;
+            const long long row = (long long)f * tok_axis<RM>(p) + gr.lin + tok0 + t;
+            const long long co = QM == kQRotHalf ? row * half : row * p.R;
             csreg[t * 128 + lane] = lane < half ? p.cosv[co + lane] : 0.0f;
             csreg[t * 128 + 64 + lane] = lane < half ? p.sinv[co + lane] : 0.0f;
         }
@@ -248,8 +298,10 @@ __device__ inline int view_vis(const DecodeParams& p, int f, int locv) {
     return v > 0 ? (int)v : 0;
 }
 
-__device__ inline int loc_of(const DecodeParams& p, int f, int w, int s) {
-    return p.loc[((long long)f * p.W + w) * p.S + s];
+// Location of token i of group g in view f (locations [F, tokens]).
+template <int RM>
+__device__ inline int loc_of(const DecodeParams& p, int f, const Grp& g, int i) {
+    return p.loc[(long long)f * tok_axis<RM>(p) + g.lin + i];
 }
 
 // Length of a row group's key space: per view, the union (max) over its tokens
@@ -257,16 +309,14 @@ __device__ inline int loc_of(const DecodeParams& p, int f, int w, int s) {
 // walks (view f's keys follow the longest range of views 0 .. f-1).  The max
 // over tokens of the per-token sum is shorter whenever different tokens see
 // most in different views, and would leave the tail of the key space unassigned.
-template <int KVM>
+template <int KVM, int RM>
 __device__ inline long long group_visible(const DecodeParams& p, int rg) {
-    const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
-    const int w = rg / nsb, sb = rg - (rg / nsb) * nsb;
-    const int s1 = (sb + 1) * kTokBlk < p.S ? (sb + 1) * kTokBlk : p.S;
+    const Grp g = group_of<RM>(p, rg);
     long long total = 0;
     for (int f = 0; f < p.F; ++f) {
         int best = 0;
-        for (int s = sb * kTokBlk; s < s1; ++s) {
-            const int v = view_vis<KVM>(p, f, loc_of(p, f, w, s));
+        for (int i = 0; i < g.ntok; ++i) {
+            const int v = view_vis<KVM>(p, f, loc_of<RM>(p, f, g, i));
             best = v > best ? v : best;
         }
         total += best;
@@ -546,15 +596,15 @@ __device__ inline void stream_range(const DecodeParams& p, const Range& r, const
 }
 
 // One workgroup: keys [v0, v1) of row group rg for KV head hkv.
-template <int DT, int QM, int KVM, bool P2>
+template <int DT, int QM, int KVM, bool P2, int RM>
 __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pages, int rg, int hkv, long long v0,
                             long long v1, bool final_out, int slot) {
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int g = lane >> 4, n = lane & 15;
-    const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
-    const int w = rg / nsb, sb = rg - (rg / nsb) * nsb;
-    const int tok0 = sb * kTokBlk + wv * kTiles;      // this wave's first token
-    const int ntile = p.S - tok0 < kTiles ? (p.S - tok0 > 0 ? p.S - tok0 : 0) : kTiles;
+    const Grp gr = group_of<RM>(p, rg);
+    const int w = gr.w;
+    const int tok0 = wv * kTiles;  // this wave's first token of the group
+    const int ntile = gr.ntok - tok0 < kTiles ? (gr.ntok - tok0 > 0 ? gr.ntok - tok0 : 0) : kTiles;
 
     Tile tl[kTiles];
 #pragma unroll
@@ -571,22 +621,21 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
         // visible keys of this view for the block (union) and per tile
         int vis_blk = 0;
         int vis_t[kTiles];
-        const int sEnd = (sb + 1) * kTokBlk < p.S ? (sb + 1) * kTokBlk : p.S;
-        for (int s = sb * kTokBlk; s < sEnd; ++s) {
-            const int v = view_vis<KVM>(p, f, loc_of(p, f, w, s));
+        for (int i = 0; i < gr.ntok; ++i) {
+            const int v = view_vis<KVM>(p, f, loc_of<RM>(p, f, gr, i));
             vis_blk = v > vis_blk ? v : vis_blk;
         }
 #pragma unroll
         for (int t = 0; t < kTiles; ++t)  // wave-uniform: the stage masks and their branches stay scalar
-            vis_t[t] = __builtin_amdgcn_readfirstlane(t < ntile ? view_vis<KVM>(p, f, loc_of(p, f, w, tok0 + t)) : 0);
+            vis_t[t] = __builtin_amdgcn_readfirstlane(t < ntile ? view_vis<KVM>(p, f, loc_of<RM>(p, f, gr, tok0 + t)) : 0);
         const long long a = v0 > P ? v0 : P;
         const long long bnd = v1 < P + vis_blk ? v1 : P + vis_blk;
         if (a < bnd) {
             u32x4 qB[kTiles][4] = {};
             // the ring is idle here (previous range drained): stage the query tiles in it
-            stage_q_tiles<DT, QM>(p, smem + wv * (kTiles * 4096),
-                                  reinterpret_cast<float*>(smem + kWaves * kTiles * 4096 + wv * kTiles * 512), w,
-                                  tok0, ntile, f, hkv, qB);
+            stage_q_tiles<DT, QM, RM>(p, smem + wv * (kTiles * 4096),
+                                      reinterpret_cast<float*>(smem + kWaves * kTiles * 4096 + wv * kTiles * 512), gr,
+                                      tok0, ntile, f, hkv, qB);
             __syncthreads();
             Range r;
             r.w = w;
@@ -647,11 +696,10 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
         if (t >= ntile) continue;
         const float lt = rows4_sum(tl[t].l);
         const float inv = lt > 0.0f ? 1.0f / lt : 0.0f;
-        const int s = tok0 + t;
         const int h = hkv * kGqa + n;
         if (final_out) {
             using raw = typename Tr<DT>::raw;
-            raw* o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+            raw* o = reinterpret_cast<raw*>(p.out) + out_row<RM>(p, gr, tok0 + t, h);
 #pragma unroll
             for (int c = 0; c < 8; ++c) {
                 const u32x2 pk = {pack2<DT>(tl[t].o[c][0] * inv, tl[t].o[c][1] * inv),
@@ -672,7 +720,7 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
 
 // P2: paged with a power-of-two block_size (shift and mask instead of a
 // division in the stage loop's row addressing).
-template <int DT, int QM, int KVM, bool P2>
+template <int DT, int QM, int KVM, bool P2, int RM>
 __global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     // the ring starts at a 256-byte aligned LDS address (the XOR addressing of
@@ -683,32 +731,30 @@ __global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
     long long* s_pref = s_scan + kWaves;
     const int NHG = p.Hkv;  // one KV head per workgroup
 
-    run_schedule(p, NHG, s_pref, s_scan, [&](int rg) { return group_visible<KVM>(p, rg); },
+    run_schedule(p, NHG, s_pref, s_scan, [&](int rg) { return group_visible<KVM, RM>(p, rg); },
                  [&](int rg, int hg, long long v0, long long v1, bool fin, int slot, long long) {
-                     chunk_piece<DT, QM, KVM, P2>(p, smem, pages, rg, hg, v0, v1, fin, slot);
+                     chunk_piece<DT, QM, KVM, P2, RM>(p, smem, pages, rg, hg, v0, v1, fin, slot);
                  });
 }
 
 // Block (segment, token of the block): thread t -> head t/16, dims [(t%16)*8, +8).
-template <int DT>
+// A segment without pieces (no visible key) writes zeros, as the decode merge does.
+template <int DT, int RM>
 __global__ __launch_bounds__(256) void dv_merge_chunk(const DecodeParams p) {
     using raw = typename Tr<DT>::raw;
     const int sg = blockIdx.x / kTokBlk;
     const int tb = blockIdx.x - sg * kTokBlk;
     const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
     if (cnt == 1) return;
-    const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
     const int NHG = p.Hkv;
     const int r = sg / NHG, hkv = sg - (sg / NHG) * NHG;
-    const int rg = p.row_begin + r;
-    const int w = rg / nsb, sb = rg - (rg / nsb) * nsb;
-    const int s = sb * kTokBlk + tb;
-    if (s >= p.S) return;
+    const Grp gr = group_of<RM>(p, p.row_begin + r);
+    if (tb >= gr.ntok) return;
     const int tid = threadIdx.x;
     const int n = tid >> 4;
     const int d = (tid & 15) * 8;
     const int h = hkv * kGqa + n;
-    raw* o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim + d;
+    raw* o = reinterpret_cast<raw*>(p.out) + out_row<RM>(p, gr, tb, h) + d;
     const int j = tb * kGqa + n;
     const int lse_off = kTokBlk * kGqa * kHeadDim + j;
     const int val_off = j * kHeadDim + d;
@@ -758,11 +804,107 @@ size_t lds_bytes(int nrows) {
     return 256 + (size_t)kRingBytes + (size_t)kPageCap * 4 + (size_t)(kWaves + nrows + 1) * sizeof(long long);
 }
 
-template <int DT, int QM, int KVM, bool P2>
+// ---- varlen row groups ----------------------------------------------------------
+//
+// Token t of a varlen call belongs to the first sequence i with
+// t < cu_seqlens_q[i + 1], or to sequence 0 when there is none (the decode
+// path's rule, varlen_paged_kernel_v21.cuh:40-47).  With M_i the running
+// maximum of cu_seqlens_q[1 .. i + 1], sequence i's tokens are therefore
+// [max(0, M_{i-1}), min(T, M_i)) (M_{-1} = 0), and the tokens from M_{W-1} on
+// form one more run, of sequence 0 -- also for tables that are not
+// non-decreasing.  Each run is cut into groups of kTokBlk tokens.  One
+// workgroup writes entry g = {first token, tokens, sequence, 0} for every
+// group, and {0, 0, 0, 0} for the entries from the group count up to gmax
+// (the host's bound T / kTokBlk + W + 1: a run of n tokens makes at most
+// n / kTokBlk + 1 groups).
+constexpr int kVgThreads = 1024;
+
+__device__ inline int block_scan_excl(int v, int* s_part, bool is_max) {
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int ident = is_max ? INT_MIN : 0;
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int o = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl = is_max ? (o > incl ? o : incl) : incl + o;
+    }
+    if (lane == 63) s_part[wv] = incl;
+    __syncthreads();
+    int before = ident;
+    for (int i = 0; i < wv; ++i) before = is_max ? (s_part[i] > before ? s_part[i] : before) : before + s_part[i];
+    const int excl_lane = __shfl_up(incl, 1, kWave);
+    const int mine = lane == 0 ? ident : excl_lane;
+    __syncthreads();
+    return is_max ? (mine > before ? mine : before) : before + mine;
+}
+
+__global__ __launch_bounds__(kVgThreads) void dv_varlen_groups(const int* cu, int W, int T, int gmax, int4* groups) {
+    __shared__ int s_m[kVarlenChunkMaxW];       // M_i
+    __shared__ int s_base[kVarlenChunkMaxW + 2];  // first group of run i (runs 0 .. W), then the total
+    __shared__ int s_part[kVgThreads / kWave];
+    const int tid = threadIdx.x;
+    // running maximum of cu[1 .. W], each thread over a contiguous block of sequences
+    const int per = (W + kVgThreads - 1) / kVgThreads;
+    const int i0 = tid * per < W ? tid * per : W, i1 = i0 + per < W ? i0 + per : W;
+    int mx = INT_MIN;
+    for (int i = i0; i < i1; ++i) {
+        const int c = cu[i + 1];
+        mx = c > mx ? c : mx;
+        s_m[i] = mx;
+    }
+    const int before = block_scan_excl(mx, s_part, true);
+    for (int i = i0; i < i1; ++i) s_m[i] = s_m[i] > before ? s_m[i] : before;
+    __syncthreads();
+    // run i (i < W: sequence i; i == W: the tokens past M_{W-1}) = [a, b)
+    auto run = [&](int i, int& a, int& b) {
+        a = i == 0 ? 0 : (s_m[i - 1] > 0 ? s_m[i - 1] : 0);
+        b = i == W ? T : (s_m[i] < T ? s_m[i] : T);
+    };
+    const int per1 = (W + 1 + kVgThreads - 1) / kVgThreads;
+    const int j0 = tid * per1 < W + 1 ? tid * per1 : W + 1, j1 = j0 + per1 < W + 1 ? j0 + per1 : W + 1;
+    int cnt = 0;
+    for (int i = j0; i < j1; ++i) {
+        int a, b;
+        run(i, a, b);
+        const int c = b > a ? (b - a + kTokBlk - 1) / kTokBlk : 0;
+        s_base[i] = c;
+        cnt += c;
+    }
+    int acc = block_scan_excl(cnt, s_part, false);
+    for (int i = j0; i < j1; ++i) {
+        const int c = s_base[i];
+        s_base[i] = acc;
+        acc += c;
+    }
+    if (tid == kVgThreads - 1) s_base[W + 1] = acc;
+    __syncthreads();
+    const int total = s_base[W + 1];
+    for (int gi = tid; gi < gmax; gi += kVgThreads) {
+        int4 e = {0, 0, 0, 0};
+        if (gi < total) {
+            // the last run whose first group is <= gi (it has groups: the next run's first is larger)
+            int lo = 0, hi = W;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (s_base[mid] <= gi) lo = mid;
+                else hi = mid - 1;
+            }
+            int a, b;
+            run(lo, a, b);
+            const int t0 = a + (gi - s_base[lo]) * kTokBlk;
+            e.x = t0;
+            e.y = b - t0 < kTokBlk ? b - t0 : kTokBlk;
+            e.z = lo == W ? 0 : lo;
+        }
+        groups[gi] = e;
+    }
+}
+
+template <int DT, int QM, int KVM, bool P2, int RM>
 hipError_t launch1(DecodeParams p, int device, int cus, long long cap, hipStream_t stream) {
     static std::atomic<unsigned long long> attr_done{0};
     hipError_t ea = once_per_device(attr_done, device, [] {
-        return hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_chunk<DT, QM, KVM, P2>),
+        return hipFuncSetAttribute(reinterpret_cast<const void*>(&dv_chunk<DT, QM, KVM, P2, RM>),
                                    hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_bytes(kMaxRows));
     });
     if (ea != hipSuccess) return ea;
@@ -770,57 +912,57 @@ hipError_t launch1(DecodeParams p, int device, int cus, long long cap, hipStream
     long long nwg = cus;  // one eight-wave workgroup per CU (LDS ring 96 KiB)
     if (nwg > cap) nwg = cap;
     p.nwg = nwg < 1 ? 1 : (int)nwg;
-    hipLaunchKernelGGL((dv_chunk<DT, QM, KVM, P2>), dim3(p.nwg), dim3(kThreads), lds, stream, p);
+    hipLaunchKernelGGL((dv_chunk<DT, QM, KVM, P2, RM>), dim3(p.nwg), dim3(kThreads), lds, stream, p);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((dv_merge_chunk<DT>), dim3(p.nrows * p.Hkv * kTokBlk), dim3(256), 0, stream, p);
+    hipLaunchKernelGGL((dv_merge_chunk<DT, RM>), dim3(p.nrows * p.Hkv * kTokBlk), dim3(256), 0, stream, p);
     return hipGetLastError();
 }
 
-template <int DT, int QM, int KVM>
+template <int DT, int QM, int KVM, int RM>
 hipError_t launch(DecodeParams p, int device, int cus, long long cap, hipStream_t stream) {
     if constexpr (KVM == kKvPaged)
-        if (p.bs_shift >= 0) return launch1<DT, QM, KVM, true>(p, device, cus, cap, stream);
-    return launch1<DT, QM, KVM, false>(p, device, cus, cap, stream);
+        if (p.bs_shift >= 0) return launch1<DT, QM, KVM, true, RM>(p, device, cus, cap, stream);
+    return launch1<DT, QM, KVM, false, RM>(p, device, cus, cap, stream);
 }
 
 }  // namespace chunk
 
 namespace {
 int chunk_cus(int device) { return device_cu_count(device); }
-}  // namespace
 
-size_t chunk_workspace_bytes(int W, int S, int Hkv, int device) {
-    if (W <= 0 || S <= 0 || Hkv <= 0) return 0;
-    const long long groups = (long long)W * ((S + chunk::kTokBlk - 1) / chunk::kTokBlk);
+// Workspace of the chunk path for `groups` row groups: partial slots, merge
+// directory, and (varlen) the group table.
+struct ChunkWs {
+    size_t part, dir, vgroups, total;
+};
+
+ChunkWs chunk_ws(long long groups, int Hkv, int device, bool varlen) {
     const long long rows = groups < kMaxRows ? groups : kMaxRows;
     const long long nseg = rows * Hkv;
     const long long slot_floats = (long long)chunk::kTokBlk * kGqa * (kHeadDim + 1);
-    const long long slots = chunk_cus(device) + nseg;
-    size_t bytes = (size_t)(slots * slot_floats * 4);
-    bytes = (bytes + 255) & ~(size_t)255;
-    bytes += (size_t)(nseg * 2 * 4);
-    return bytes;
+    ChunkWs l;
+    l.part = ((size_t)((chunk_cus(device) + nseg) * slot_floats * 4) + 255) & ~(size_t)255;
+    l.dir = ((size_t)(nseg * 2 * 4) + 255) & ~(size_t)255;
+    l.vgroups = varlen ? (size_t)groups * 16 : 0;
+    l.total = l.part + l.dir + l.vgroups;
+    return l;
 }
 
-hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& base, long long max_keys_per_group,
-                        void* workspace, size_t ws_bytes, hipStream_t stream) {
-    if (base.W <= 0 || base.S <= 0 || base.Hkv <= 0) return hipSuccess;
+long long varlen_gmax(int T, int W) { return (long long)T / chunk::kTokBlk + W + 1; }
+
+// The chunk launches over `groups` row groups, kMaxRows at a time.
+template <int RM>
+hipError_t launch_groups(int dtype, int qmode, int kvmode, DecodeParams p, long long groups_total,
+                         long long max_keys_per_group, const ChunkWs& l, void* workspace, hipStream_t stream) {
     int device = 0;
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return e;
     const int cus = chunk_cus(device);
-    DecodeParams p = base;
     p.hpw = 1;
     p.slot_floats = chunk::kTokBlk * kGqa * (kHeadDim + 1);
-    const long long groups_total = (long long)p.W * ((p.S + chunk::kTokBlk - 1) / chunk::kTokBlk);
-    const long long rows_cap = groups_total < kMaxRows ? groups_total : kMaxRows;
-    const long long nseg_cap = rows_cap * p.Hkv;
-    size_t part_bytes = (size_t)((cus + nseg_cap) * p.slot_floats * 4);
-    part_bytes = (part_bytes + 255) & ~(size_t)255;
-    if (ws_bytes < part_bytes + (size_t)nseg_cap * 2 * 4) return hipErrorInvalidValue;
     p.part = reinterpret_cast<float*>(workspace);
-    p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
+    p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + l.part);
     p.piece_cost = chunk::kPieceCost;
     // odd workgroups (odd XCD of each pair) take shorter chunks, as in the decode
     // split; 30 per mille measured best on configuration 5
@@ -830,19 +972,72 @@ hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& ba
         p.row_begin = (int)g0;
         p.nrows = (int)(groups_total - g0 < kMaxRows ? groups_total - g0 : kMaxRows);
         const long long cap = ((long long)p.nrows * p.Hkv * max_keys_per_group + p.min_keys - 1) / p.min_keys;
-        if (dtype == kBF16 && qmode == kQRotFull && kvmode == kKvPaged)
-            e = chunk::launch<kBF16, kQRotFull, kKvPaged>(p, device, cus, cap, stream);
-        else if (dtype == kF16 && qmode == kQRotFull && kvmode == kKvPaged)
-            e = chunk::launch<kF16, kQRotFull, kKvPaged>(p, device, cus, cap, stream);
-        else if (dtype == kBF16 && qmode == kQPre && kvmode == kKvContig)
-            e = chunk::launch<kBF16, kQPre, kKvContig>(p, device, cus, cap, stream);
-        else if (dtype == kF16 && qmode == kQPre && kvmode == kKvContig)
-            e = chunk::launch<kF16, kQPre, kKvContig>(p, device, cus, cap, stream);
-        else
-            e = hipErrorInvalidValue;
+        if (RM == kRowVarlen) {
+            if (dtype == kBF16 && qmode == kQRotHalf && kvmode == kKvPaged)
+                e = chunk::launch<kBF16, kQRotHalf, kKvPaged, RM>(p, device, cus, cap, stream);
+            else if (dtype == kF16 && qmode == kQRotHalf && kvmode == kKvPaged)
+                e = chunk::launch<kF16, kQRotHalf, kKvPaged, RM>(p, device, cus, cap, stream);
+            else
+                e = hipErrorInvalidValue;
+        } else {
+            if (dtype == kBF16 && qmode == kQRotFull && kvmode == kKvPaged)
+                e = chunk::launch<kBF16, kQRotFull, kKvPaged, RM>(p, device, cus, cap, stream);
+            else if (dtype == kF16 && qmode == kQRotFull && kvmode == kKvPaged)
+                e = chunk::launch<kF16, kQRotFull, kKvPaged, RM>(p, device, cus, cap, stream);
+            else if (dtype == kBF16 && qmode == kQPre && kvmode == kKvContig)
+                e = chunk::launch<kBF16, kQPre, kKvContig, RM>(p, device, cus, cap, stream);
+            else if (dtype == kF16 && qmode == kQPre && kvmode == kKvContig)
+                e = chunk::launch<kF16, kQPre, kKvContig, RM>(p, device, cus, cap, stream);
+            else
+                e = hipErrorInvalidValue;
+        }
         if (e != hipSuccess) return e;
     }
     return hipSuccess;
+}
+}  // namespace
+
+size_t chunk_workspace_bytes(int W, int S, int Hkv, int device) {
+    if (W <= 0 || S <= 0 || Hkv <= 0) return 0;
+    const long long groups = (long long)W * ((S + chunk::kTokBlk - 1) / chunk::kTokBlk);
+    return chunk_ws(groups, Hkv, device, false).total;
+}
+
+hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& base, long long max_keys_per_group,
+                        void* workspace, size_t ws_bytes, hipStream_t stream) {
+    if (base.W <= 0 || base.S <= 0 || base.Hkv <= 0) return hipSuccess;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    const long long groups = (long long)base.W * ((base.S + chunk::kTokBlk - 1) / chunk::kTokBlk);
+    const ChunkWs l = chunk_ws(groups, base.Hkv, device, false);
+    if (ws_bytes < l.total) return hipErrorInvalidValue;
+    return launch_groups<kRowWS>(dtype, qmode, kvmode, base, groups, max_keys_per_group, l, workspace, stream);
+}
+
+size_t varlen_chunk_workspace_bytes(int T, int W, int Hkv, int device) {
+    if (T <= 0 || W <= 0 || Hkv <= 0) return 0;
+    return chunk_ws(varlen_gmax(T, W), Hkv, device, true).total;
+}
+
+hipError_t launch_varlen_chunk(int dtype, const DecodeParams& base, long long max_keys_per_group, void* workspace,
+                               size_t ws_bytes, hipStream_t stream) {
+    if (base.T <= 0 || base.W <= 0 || base.Hkv <= 0) return hipSuccess;
+    if (base.W > kVarlenChunkMaxW) return hipErrorInvalidValue;
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return e;
+    const long long gmax = varlen_gmax(base.T, base.W);
+    const ChunkWs l = chunk_ws(gmax, base.Hkv, device, true);
+    if (ws_bytes < l.total) return hipErrorInvalidValue;
+    DecodeParams p = base;
+    int4* groups = reinterpret_cast<int4*>(reinterpret_cast<unsigned char*>(workspace) + l.part + l.dir);
+    p.vgroups = reinterpret_cast<const int*>(groups);
+    hipLaunchKernelGGL(chunk::dv_varlen_groups, dim3(1), dim3(chunk::kVgThreads), 0, stream, base.cu_q, base.W,
+                       base.T, (int)gmax, groups);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_groups<kRowVarlen>(dtype, kQRotHalf, kKvPaged, p, gmax, max_keys_per_group, l, workspace, stream);
 }
 
 }  // namespace dv

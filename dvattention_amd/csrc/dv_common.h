@@ -63,6 +63,7 @@ struct DecodeParams {
     const void* vc;
     const int* bt;
     const int* cu_q;
+    const int* vgroups;   // varlen chunk path: per row group {first token, tokens, sequence, 0}
     const FragDesc* frag_tab;  // device table when F > kMaxFragArgs
     float l2scale;        // softmax scale / ln(2): scores are kept in base-2 units
     int F, W, S, Hq, Hkv, R;
@@ -187,6 +188,16 @@ inline bool use_chunk(int dtype, int S) { return S >= 2 && dtype != kF32; }
 size_t chunk_workspace_bytes(int W, int S, int Hkv, int device);
 hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& base, long long max_keys_per_group,
                         void* workspace, size_t ws_bytes, hipStream_t stream);
+// Varlen calls whose packed tokens average two or more per sequence go through
+// the chunk kernel too: the tokens of each sequence (token t: the first i with
+// t < cu_seqlens_q[i + 1]) in groups of up to 16, one K/V stream per group.
+constexpr int kVarlenChunkMaxW = 4096;  // sequences of the group-table pass (LDS)
+inline bool use_varlen_chunk(int dtype, int T, int W) {
+    return dtype != kF32 && W >= 1 && W <= kVarlenChunkMaxW && (long long)T >= 2ll * W;
+}
+size_t varlen_chunk_workspace_bytes(int T, int W, int Hkv, int device);
+hipError_t launch_varlen_chunk(int dtype, const DecodeParams& base, long long max_keys_per_group, void* workspace,
+                               size_t ws_bytes, hipStream_t stream);
 // Single-launch path (contiguous views, any dtype): chunks per item for F views of
 // fragment_tokens toks, or -1 when the views are too many or too long; the
 // workspace it needs for `items` (row, KV head) items; the launch (qmode kQPre

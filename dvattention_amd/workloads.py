@@ -220,6 +220,45 @@ def config(i: int, device="cuda", seed=1234) -> Workload:
     raise ValueError(f"no config {i}")
 
 
+def as_varlen(wl: Workload) -> Workload:
+    """The same problem through ``dvattn_varlen_paged_sdpa``: a paged workload's
+    S query tokens per sequence packed as T = W*S tokens (cu_seqlens_q =
+    S * arange(W + 1)), locations ``[F,T]``, half-width cos/sin ``[F,T,R/2]``
+    (the first R/2 entries of each full-width row), queries ``[T,Hq,E]``.  The
+    output ``[T,Hq,E]`` is the paged output with its S axis moved next to W."""
+    assert wl.op == "paged"
+    t = wl.t
+    W, S, R = wl.meta["W"], wl.meta["S"], wl.meta["R"]
+    F = t["locations"].shape[0]
+    T = W * S
+    Hq = t["queries"].shape[1]
+    dev = t["queries"].device
+    vt = {
+        "queries": t["queries"].permute(0, 2, 1, 3).reshape(T, Hq, -1).contiguous(),
+        "locations": t["locations"].reshape(F, T).contiguous(),
+        "cosines": t["cosines"].reshape(F, T, R)[..., : R // 2].contiguous(),
+        "sines": t["sines"].reshape(F, T, R)[..., : R // 2].contiguous(),
+        "fragment_lengths": t["fragment_lengths"],
+        "k_cache": t["k_cache"],
+        "v_cache": t["v_cache"],
+        "block_tables": t["block_tables"],
+        "cu_seqlens_q": (S * torch.arange(W + 1, dtype=torch.int32)).to(dev),
+        "cu_seqlens_k": torch.zeros(W + 1, dtype=torch.int32, device=dev),
+    }
+    cs = 2 * F * T * (R // 2) * 4
+    alg = wl.alg_bytes - 2 * F * T * R * 4 + cs + (W + 1) * 4
+    meta = dict(wl.meta, out_shape=(T, Hq, t["queries"].shape[-1]), T=T, paged_name=wl.name)
+    return Workload(wl.name.replace("cfg5_chunk", "cfg5v_varlen_chunk"), "varlen", wl.dtype, wl.scale, vt, alg,
+                    wl.flops, meta)
+
+
+def workload(key, device="cuda", seed=1234) -> Workload:
+    """A configuration by key: 1-5, or "5v" (configuration 5 through the varlen op)."""
+    if str(key) == "5v":
+        return as_varlen(config(5, device=device, seed=seed))
+    return config(int(key), device=device, seed=seed)
+
+
 def run(wl: Workload, out: torch.Tensor | None = None, rq: torch.Tensor | None = None):
     """Run a workload through the torch operator API of dvattention_amd."""
     from . import attention as A

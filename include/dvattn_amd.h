@@ -147,7 +147,10 @@ DVATTN_API dvattn_status dvattn_paged_sdpa_noalloc(int dtype, void* out, float s
  * queries [T,Hq,E] T; cosines/sines [F,T,R/2] f32 (half width);
  * cu_seqlens_q [W+1] i32: token t belongs to the first sequence i with
  * t < cu_seqlens_q[i+1] (sequence 0 if none); cu_seqlens_k is accepted and,
- * as in the reference (binding.cu:279,290), not read.
+ * as in the reference (binding.cu:279,290), not read.  16-bit calls with
+ * T >= 2W (and W <= 4096) read each sequence's K/V once per group of up to 16
+ * of its tokens (the workspace size follows the same rule); other calls once
+ * per token, as the reference does.
  * Replaces binding.cu:249-296 / varlen_paged_kernel_v21.cuh:373-428. */
 DVATTN_API size_t dvattn_varlen_paged_sdpa_workspace_size(int dtype, const dvattn_shape* shape, int device);
 DVATTN_API dvattn_status dvattn_varlen_paged_sdpa(int dtype, void* out, float scale, const int* locations,

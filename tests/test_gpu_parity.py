@@ -383,6 +383,13 @@ VARLEN_CASES = [
     (3, 3, 6, [0, 4, 2, 5], 2, 16, [20, 6, 33], 32),      # malformed cu_seqlens_q
     (1, 2, 3, [0, 1, 2], 1, 3, [50], 0),
     (6, 2, 3, [0, 2, 3], 2, 16, [40, 0, 90, 17, 64, 5], 64),
+    # T >= 2W: each sequence's tokens share one K/V stream (groups of <= 16)
+    (2, 4, 40, [0, 16, 17, 33, 40], 2, 16, [300, 250], 64),
+    (1, 2, 50, [0, 33, 50], 8, 16, [700], 128),
+    (2, 4, 30, [0, 10, -3, 25, 12], 1, 16, [200, 64], 32),  # malformed: empty runs, trailing tokens -> sequence 0
+    (1, 3, 12, [0, 5, 20, 30], 2, 8, [150], 64),              # table past T
+    (1, 2, 9, [0, 0, 0], 1, 16, [100], 64),                   # every token past the table -> sequence 0
+    (3, 1, 64, [0, 64], 1, 1, [90, 0, 45], 16),               # one sequence, four groups, block size 1
 ]
 
 

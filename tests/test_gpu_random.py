@@ -2,8 +2,11 @@
 paged, varlen and contiguous (dvattn_sdpa) with random view counts, lengths
 (including empty views), locations (including negative and past-the-end),
 block sizes, KV heads, query tokens per sequence (S = 1 takes the decode
-kernels, S >= 2 the multi-query kernel for 16-bit types) and dtypes.  Each case
-is small enough for the oracle to finish in well under a second.
+kernels, S >= 2 the multi-query kernel for 16-bit types; varlen calls with two
+or more packed tokens per sequence on average take the multi-query kernel too,
+in groups of up to 16 tokens of one sequence, including runs of 16 and 17 and
+malformed cu_seqlens_q tables) and dtypes.  Each case is small enough for the
+oracle to finish in well under a second.
 
 DVATTN_RANDOM_CASES (default 200) and DVATTN_RANDOM_SEED0 (default 0) widen or
 move the sweep; the default run is the one the suite commits to.
@@ -56,11 +59,13 @@ def test_random_paged(dv, gpu, seed):
 def test_random_varlen(dv, gpu, seed):
     rng, F, lens, dtype, Hkv = draw(seed)
     W = int(rng.integers(1, 5))
-    counts = rng.integers(0, 3, size=W)
+    counts = rng.choice([0, 1, 1, 2, 2, 5, 16, 17], size=W)
     cu = [0] + np.cumsum(counts).tolist()
     T = max(int(cu[-1]), 1)
     if cu[-1] == 0:
         cu[-1] = 1
+    if rng.random() < 0.2:  # a malformed table (tokens map by the first i with t < cu[i + 1])
+        cu[int(rng.integers(1, W + 1))] = int(rng.integers(-2, T + 6))
     bs = int(rng.choice([1, 4, 16]))
     R = int(rng.choice([16, 64, 128]))
     d = rand_varlen(F, W, T, cu, Hkv, bs, lens, R, dtype, seed=seed)

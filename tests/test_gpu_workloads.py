@@ -3,7 +3,10 @@ the inputs bench.py times): every output row of the HIP call against the CPU
 oracle, run batch by batch on just those rows (their queries, locations,
 cos/sin and the pages their block tables name, remapped into a compact cache),
 and a second call bit-identical to the first.  Tolerance rule of
-test_gpu_parity.close.
+test_gpu_parity.close.  "5v" is configuration 5 packed through the varlen op
+(cu_seqlens_q = 16 * arange(17), half-width cos/sin): every token against the
+oracle, and bit-identical to the paged call (the same 16-token groups, the same
+work split).
 """
 import numpy as np
 import pytest
@@ -86,3 +89,42 @@ def test_config_rows_vs_oracle(gpu, cfg, batch):
     else:
         ref = O.varlen_paged_sdpa(wl.scale, **varlen_rows(wl, rows, gpu))
     close(out[torch.tensor(rows).to(gpu)], ref, wl.dtype, f"config {cfg} rows {rows[0]}-{rows[-1]}")
+
+
+def varlen5_out(gpu):
+    """(varlen workload, output) of configuration 5 packed as varlen tokens."""
+    if "5v" not in _cache:
+        from dvattention_amd import workloads as WL
+        _cache.clear()
+        torch.cuda.empty_cache()
+        wl = WL.config(5, device=gpu, seed=4321)
+        vw = WL.as_varlen(wl)
+        out = WL.run(vw)
+        paged = WL.run(wl)
+        torch.cuda.synchronize()
+        again = WL.run(vw)
+        torch.cuda.synchronize()
+        assert torch.equal(out, again), "repeat call differs"
+        W, S = wl.meta["W"], wl.meta["S"]
+        same = out.reshape(W, S, out.shape[1], out.shape[2]).permute(0, 2, 1, 3)
+        assert torch.equal(same, paged), "varlen-packed configuration 5 differs from the paged call"
+        del wl, paged
+        _cache["5v"] = (vw, out)
+    return _cache["5v"]
+
+
+@pytest.mark.parametrize("batch", range(2))
+def test_config5_varlen_rows_vs_oracle(gpu, batch):
+    vw, out = varlen5_out(gpu)
+    S = vw.meta["S"]
+    seqs = list(range(batch * 8, (batch + 1) * 8))
+    toks = torch.tensor([w * S + s for w in seqs for s in range(S)]).to(gpu)
+    t = vw.t
+    kc, vc, bt = compact_pages(t, torch.tensor(seqs).to(gpu), gpu)
+    d = dict(locations=t["locations"][:, toks].cpu(), queries=t["queries"][toks].cpu(),
+             cosines=t["cosines"][:, toks].cpu(), sines=t["sines"][:, toks].cpu(),
+             fragment_lengths=t["fragment_lengths"].cpu(), k_cache=kc, v_cache=vc, block_tables=bt,
+             cu_seqlens_q=(S * torch.arange(len(seqs) + 1)).to(torch.int32),
+             cu_seqlens_k=torch.zeros(len(seqs) + 1, dtype=torch.int32))
+    ref = O.varlen_paged_sdpa(vw.scale, **d)
+    close(out[toks], ref, vw.dtype, f"config 5 (varlen) sequences {seqs[0]}-{seqs[-1]}")
