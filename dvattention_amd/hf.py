@@ -20,6 +20,13 @@ What changes against the reference, and why:
   lengths and orders.
 * The attention is ``dvattn_fused`` as in the reference's non-eager path
   (attention.py:319-331).
+* ``DVAttnCache`` and ``merge_caches`` also take transformers ``Cache`` objects,
+  as the reference's do (attention.py:109-118, 245-251).  Their contents are
+  copied once into a pool the cache creates (it grows when a segment fills),
+  and each caller cache is rebound to views of its segment.  Its layers then
+  show every appended token, and its ``get_seq_length`` stays correct without
+  a second copy.  A later ``DVAttnCache`` or ``merge_caches`` call on the same
+  cache objects finds their segments again.
 
 The three device operations are reached through an ``ops`` object (default:
 this package's HIP operators), so the module code can also be driven by a
@@ -27,6 +34,7 @@ checker implementation in tests.
 """
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 from typing import Any, Dict, List, Optional
 
@@ -76,9 +84,45 @@ class SegmentPool:
         self.k = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(self.num_layers)]
         self.v = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(self.num_layers)]
         self.segments = [Segment(self, i) for i in range(num_segments)]
+        self.growable = False   # pools made for caller caches grow when a segment fills
+        self.mirrors = []       # (weak reference to a caller cache, its segment)
 
     def __getitem__(self, i: int) -> "Segment":
         return self.segments[i]
+
+    def resize(self, num_segments: Optional[int] = None, capacity: Optional[int] = None) -> None:
+        """Reallocate with more segments and/or a larger capacity, keeping every
+        segment's tokens; the caller caches bound to this pool are rebound."""
+        n0 = len(self.segments)
+        n = max(n0, num_segments or n0)
+        cap = max(self.capacity, capacity or self.capacity)
+        if n == n0 and cap == self.capacity:
+            return
+        for layer in range(self.num_layers):
+            for name in ("k", "v"):
+                old = getattr(self, name)[layer]
+                new = torch.zeros((n, self.Hkv, cap, self.E), dtype=old.dtype, device=old.device)
+                new[:n0, :, :self.capacity].copy_(old)
+                getattr(self, name)[layer] = new
+        self.capacity = cap
+        self.segments += [Segment(self, i) for i in range(n0, n)]
+        for layer in range(self.num_layers):
+            self.sync_mirrors(layer)
+
+    def sync_mirrors(self, layer: int, only=None) -> None:
+        """Rebind the caller caches of this pool (those of segments ``only``) to
+        views of their segments' filled part of ``layer``."""
+        live = []
+        for ref, seg in self.mirrors:
+            cache = ref()
+            if cache is None:
+                continue
+            live.append((ref, seg))
+            if only is None or any(seg is o for o in only):
+                L = seg.get_seq_length(layer)
+                _set_cache_layer(cache, layer, self.k[layer][seg.index:seg.index + 1, :, :L],
+                                 self.v[layer][seg.index:seg.index + 1, :, :L])
+        self.mirrors = live
 
 
 class Segment:
@@ -102,10 +146,100 @@ class Segment:
 
 def _cache_layer(cache, layer: int):
     """(keys, values) ``[1, Hkv, L, E]`` of one layer of a transformers cache
-    (``layers[i].keys`` in transformers 5, ``key_cache[i]`` before)."""
+    (``layers[i].keys`` in transformers 5, ``key_cache[i]`` before), or
+    (None, None) for a layer the cache has not filled yet."""
     if hasattr(cache, "layers"):
+        if layer >= len(cache.layers) or not getattr(cache.layers[layer], "is_initialized", True):
+            return None, None
         return cache.layers[layer].keys, cache.layers[layer].values
+    if layer >= len(cache.key_cache):
+        return None, None
     return cache.key_cache[layer], cache.value_cache[layer]
+
+
+def _set_cache_layer(cache, layer: int, k: torch.Tensor, v: torch.Tensor) -> None:
+    """Make ``k``/``v`` the contents of one layer of a transformers cache."""
+    if hasattr(cache, "layers"):
+        while len(cache.layers) <= layer:
+            make = getattr(cache, "layer_class_to_replicate", None)
+            if make is None:
+                from transformers.cache_utils import DynamicLayer as make
+            cache.layers.append(make())
+        lay = cache.layers[layer]
+        lay.keys, lay.values = k, v
+        lay.dtype, lay.device = k.dtype, k.device
+        lay.is_initialized = True
+    else:
+        while len(cache.key_cache) <= layer:
+            cache.key_cache.append(k[:, :, :0])
+            cache.value_cache.append(v[:, :, :0])
+        cache.key_cache[layer], cache.value_cache[layer] = k, v
+
+
+# caller cache -> its segment, for caches a DVAttnCache has taken into a pool
+_POOLED = weakref.WeakKeyDictionary()
+
+
+def _segment_of(x) -> Optional["Segment"]:
+    if isinstance(x, Segment):
+        return x
+    try:
+        return _POOLED.get(x)
+    except TypeError:
+        return None
+
+
+def _rotary(model):
+    """The rotary embedding of ``model``: a causal-LM wrapper (``model.model``)
+    or the decoder itself, as the reference's merge_caches is given."""
+    rot = getattr(model, "rotary_emb", None)
+    return rot if rot is not None else model.model.rotary_emb
+
+
+def _config(model):
+    inner = model.model if hasattr(model, "model") and hasattr(model.model, "layers") else model
+    return inner.config
+
+
+def pool_caches(caches, model, capacity: Optional[int] = None) -> List["Segment"]:
+    """The segments of transformers caches ``caches``.  Caches already in a
+    pool keep their segments; the others are copied into that pool (new
+    segments), or into a new one.  Afterwards every cache's layers are views of
+    its segment.  The pool holds ``capacity`` tokens per segment (default:
+    the longest cache plus 1024, rounded up to a power of two) and doubles when
+    an append or merge would overflow it."""
+    pools = {id(_segment_of(c).pool): _segment_of(c).pool for c in caches if _segment_of(c) is not None}
+    if len(pools) > 1:
+        raise ValueError("DVAttnCache: the caches belong to different pools (different DVAttnCache structures "
+                         "that were never merged)")
+    fresh = []
+    for c in caches:
+        if _segment_of(c) is None and not any(c is f for f in fresh):
+            fresh.append(c)
+    cfg = _config(model)
+    n_layers = cfg.num_hidden_layers
+    lengths = [max((_cache_layer(c, l)[0].shape[2] for l in range(n_layers) if _cache_layer(c, l)[0] is not None),
+                   default=0) for c in fresh]
+    if pools:
+        pool = next(iter(pools.values()))
+        first = len(pool.segments)
+        pool.resize(num_segments=first + len(fresh), capacity=max(lengths, default=0))
+    else:
+        ref = next((_cache_layer(c, 0)[0] for c in fresh if _cache_layer(c, 0)[0] is not None), None)
+        if ref is None:
+            ref = next(model.parameters())
+        need = max(lengths, default=0) + 1024
+        cap = capacity if capacity is not None else 1 << (need - 1).bit_length()
+        pool = SegmentPool(cfg, len(fresh), max(cap, max(lengths, default=0)), ref.dtype, ref.device)
+        pool.growable = True
+        first = 0
+    segs = segments_from_caches(fresh, pool, first)
+    for c, seg in zip(fresh, segs):
+        _POOLED[c] = seg
+        pool.mirrors.append((weakref.ref(c), seg))
+    for layer in range(pool.num_layers):
+        pool.sync_mirrors(layer, only=segs)
+    return [_segment_of(c) for c in caches]
 
 
 def segments_from_caches(caches, pool: SegmentPool, first: int = 0) -> List[Segment]:
@@ -120,6 +254,9 @@ def segments_from_caches(caches, pool: SegmentPool, first: int = 0) -> List[Segm
         seg = pool[first + j]
         for layer in range(pool.num_layers):
             k, v = _cache_layer(cache, layer)
+            if k is None or k.numel() == 0:
+                seg.lengths[layer] = 0
+                continue
             if k.dim() != 4 or k.shape[0] != 1:
                 raise ValueError(f"cache {j} layer {layer}: expected keys [1, Hkv, L, E], got {tuple(k.shape)}")
             L = k.shape[2]
@@ -137,14 +274,23 @@ class DVAttnCache:
 
     ``cache_structure[w]`` lists the segments worker w attends to, in its own
     order (its own segment, where its new tokens go, last by default:
-    ``write_to``).  All segments must come from one ``SegmentPool``.  Unlike the
-    reference, a worker may leave out segments other workers list; it does not
-    see them.
+    ``write_to``).  The entries are segments of one ``SegmentPool``, or -- the
+    reference's signature -- transformers ``Cache`` objects (``DynamicCache``),
+    which are taken into a pool (``pool_caches``) and kept showing their
+    segments' tokens.  Unlike the reference, a worker may leave out segments
+    other workers list; it does not see them.
     """
 
-    def __init__(self, cache_structure: List[List[Segment]], model, write_to: Optional[List[Segment]] = None,
-                 ops=HipOps):
+    def __init__(self, cache_structure: List[List[Any]], model, write_to: Optional[List[Any]] = None,
+                 ops=HipOps, capacity: Optional[int] = None):
         self.model = model.model
+        if not all(isinstance(x, Segment) for cl in cache_structure for x in cl) or \
+                (write_to and not all(isinstance(x, Segment) for x in write_to)):
+            flat = [x for cl in cache_structure for x in cl] + list(write_to or [])
+            segs = pool_caches(flat, model, capacity)
+            it = iter(segs)
+            cache_structure = [[next(it) for _ in cl] for cl in cache_structure]
+            write_to = [next(it) for _ in write_to] if write_to else None
         self.cache_structure = cache_structure
         self.write_to = write_to if write_to else [cl[-1] for cl in cache_structure]
         self.pool = cache_structure[0][0].pool
@@ -190,8 +336,10 @@ class DVAttnCache:
                 seg = self.write_to[w]
                 base = next_pos.get(id(seg), seg.get_seq_length(0))
                 if base + n > self.pool.capacity:
-                    raise RuntimeError(f"segment {seg.index} is full ({base} + {n} > "
-                                       f"{self.pool.capacity} tokens)")
+                    if not self.pool.growable:
+                        raise RuntimeError(f"segment {seg.index} is full ({base} + {n} > "
+                                           f"{self.pool.capacity} tokens)")
+                    self.pool.resize(capacity=1 << (base + n - 1).bit_length())
                 pos[w, S - n:] = torch.arange(base, base + n, dtype=torch.int32)
                 next_pos[id(seg)] = base + n
             self._n_new = [int(n) for n in n_new]
@@ -203,6 +351,8 @@ class DVAttnCache:
         self.ops.kv_append(key_states, value_states, self._positions, cos, sin, pages_k, pages_v, self._wt_table)
         for w in range(W):
             self.write_to[w].lengths[layer_idx] += self._n_new[w]
+        if self.pool.mirrors:
+            self.pool.sync_mirrors(layer_idx, only=self.write_to)
 
         if layer_idx == 0:
             # views in the order of worker 0's structure (attention.py:158-166), then
@@ -269,26 +419,58 @@ class DVAttnCache:
         }
 
 
-def merge_caches(target: Segment, source: Segment, model, ops=HipOps) -> None:
+def merge_caches(target, source, model, ops=HipOps) -> None:
     """Append ``source`` to ``target`` with its keys re-rotated by the target's
-    length (attention.py:245-251): one append per layer with a single cos/sin row."""
-    assert target.pool is source.pool
-    pool = target.pool
-    rot = model.model.rotary_emb
-    L = source.get_seq_length(0)
+    length (attention.py:245-251).  ``target`` and ``source`` are segments or
+    transformers caches; ``model`` the causal LM or its decoder (the reference
+    passes the decoder).  A target in a pool (a segment, or a cache a
+    DVAttnCache took in) gets one append per layer with a single cos/sin row,
+    the pool growing if it must; a plain target cache gets the reference's own
+    steps: the source's keys rotated in PyTorch, then ``target.update``."""
+    rot = _rotary(model)
+    t_seg, s_seg = _segment_of(target), _segment_of(source)
+    n_layers = _config(model).num_hidden_layers
+
+    def source_layer(layer):
+        if s_seg is not None:
+            L = s_seg.get_seq_length(layer)
+            return s_seg.keys(layer)[:, :, :L], s_seg.values(layer)[:, :, :L]
+        return _cache_layer(source, layer)
+
+    if t_seg is None:
+        k0, _ = source_layer(0)
+        Ls = 0 if k0 is None else k0.shape[2]
+        if Ls == 0:
+            return
+        lt = target.get_seq_length()
+        cos, sin = rot(k0, torch.full((1, Ls), lt, dtype=torch.int64, device=k0.device))
+        for layer in range(n_layers):
+            k, v = source_layer(layer)
+            target.update(_A.apply_rotary_pos_emb(k, cos, sin), v, layer)
+        return
+    pool = t_seg.pool
     dev = pool.k[0].device
     for layer in range(pool.num_layers):
-        t0 = target.get_seq_length(layer)
+        k, v = source_layer(layer)
+        L = 0 if k is None else k.shape[2]
+        if L == 0:
+            continue
+        t0 = t_seg.get_seq_length(layer)
         if t0 + L > pool.capacity:
-            raise RuntimeError("merge_caches: target segment is full")
-        ref = pool.k[layer]
-        cos, sin = rot(ref, torch.full((1, 1), t0, dtype=torch.int64, device=dev))
+            if not pool.growable:
+                raise RuntimeError("merge_caches: target segment is full")
+            pool.resize(capacity=1 << (t0 + L - 1).bit_length())
+            if s_seg is not None and s_seg.pool is pool:
+                k, v = source_layer(layer)
+        cos, sin = rot(pool.k[layer], torch.full((1, 1), t0, dtype=torch.int64, device=dev))
         pos = (t0 + torch.arange(L, dtype=torch.int32, device=dev)).reshape(1, L)
-        table = torch.tensor([[target.index]], dtype=torch.int32, device=dev)
-        ops.kv_append(source.keys(layer)[:, :, :L], source.values(layer)[:, :, :L], pos, cos.reshape(1, 1, -1),
-                      sin.reshape(1, 1, -1), pool.k[layer].permute(0, 2, 1, 3), pool.v[layer].permute(0, 2, 1, 3),
-                      table)
-        target.lengths[layer] += L
+        table = torch.tensor([[t_seg.index]], dtype=torch.int32, device=dev)
+        ops.kv_append(k.to(device=dev, dtype=pool.k[layer].dtype), v.to(device=dev, dtype=pool.v[layer].dtype), pos,
+                      cos.reshape(1, 1, -1), sin.reshape(1, 1, -1), pool.k[layer].permute(0, 2, 1, 3),
+                      pool.v[layer].permute(0, 2, 1, 3), table)
+        t_seg.lengths[layer] += L
+        if pool.mirrors:
+            pool.sync_mirrors(layer, only=[t_seg])
 
 
 class AttentionModule(nn.Module):
@@ -358,4 +540,4 @@ def model_surgery(model) -> None:
 
 
 __all__ = ["CacheStructure", "SegmentPool", "Segment", "DVAttnCache", "merge_caches", "AttentionModule",
-           "model_surgery", "HipOps", "segments_from_caches"]
+           "model_surgery", "HipOps", "segments_from_caches", "pool_caches"]

@@ -11,9 +11,11 @@ library raises ``ImportError``.  The names are the reference's:
   ``dvattn_rope``, ``rotate_half``, ``apply_rotary_pos_emb`` (attention.py:17-88),
   plus the paged / varlen wrappers of this build;
 * model integration -- ``CacheStructure``, ``DVAttnCache``, ``merge_caches``,
-  ``AttentionModule``, ``model_surgery`` (attention.py:100-343), whose
-  segments are ``SegmentPool`` slices (``segments_from_caches`` fills them from
-  transformers caches).
+  ``AttentionModule``, ``model_surgery`` (attention.py:100-343).  As in the
+  reference, ``DVAttnCache(cache_structure, model, write_to)`` and
+  ``merge_caches(target, source, model)`` take transformers ``Cache`` objects;
+  they also take ``SegmentPool`` segments, the storage the caches are moved
+  into.
 """
 from dvattention_amd.attention import (  # noqa: F401  (importing dvattention_amd registers the ops)
     apply_rotary_pos_emb,

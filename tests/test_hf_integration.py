@@ -225,6 +225,89 @@ def test_segments_from_transformers_caches_cpu():
         assert torch.allclose(o[0, -1], ref[9 + i], atol=1e-4, rtol=1e-4), i
 
 
+def reference_caller(model, ops, prompt, own, nxt, capacity=None, stock=None):
+    """The reference's call shape (attention.py:109-118, 208-251) on transformers
+    caches: a prompt cache filled through a one-worker DVAttnCache on an empty
+    DynamicCache (or by the unmodified model ``stock``, transformers itself),
+    two workers with empty DynamicCaches that each see [prompt, own],
+    ``merge_caches(prompt_cache, worker0_cache, decoder)``, then one more token
+    on the merged cache.  Returns the logits of every step and the caches."""
+    from transformers import DynamicCache
+
+    from dvattention_amd import hf
+    if stock is not None:
+        with torch.no_grad():
+            pre = stock(input_ids=prompt[None], use_cache=True).past_key_values
+    else:
+        pre = DynamicCache()
+        run_steps(model, hf.DVAttnCache([[pre]], model, ops=ops), [prompt[None]])
+    w0, w1 = DynamicCache(), DynamicCache()
+    cache = hf.DVAttnCache([[pre, w0], [pre, w1]], model, ops=ops, capacity=capacity)
+    outs = run_steps(model, cache, [own[:, i:i + 1] for i in range(own.shape[1])])
+    hf.merge_caches(pre, w0, model.model, ops=ops)
+    solo = hf.DVAttnCache([[pre, DynamicCache()]], model, ops=ops)
+    outs += run_steps(model, solo, [nxt[None, None]])
+    return outs, pre, w0, w1
+
+
+def test_reference_signature_with_transformers_caches_cpu():
+    """DVAttnCache / merge_caches driven with transformers DynamicCaches in the
+    reference's call shape: each worker decodes like transformers on [prompt,
+    own], the caller's caches show the appended tokens (their own keys rotated
+    at worker-local positions), and after the merge the prompt cache holds the
+    worker's keys re-rotated to absolute positions -- transformers' own cache of
+    the concatenated sequence -- and decodes the next token like it."""
+    model = tiny_qwen2(torch.float32, "cpu")
+    ours = surgery_copy(model)
+    g = torch.Generator().manual_seed(12)
+    P, n = 9, 3
+    prompt = torch.randint(0, 320, (P,), generator=g)
+    own = torch.randint(0, 320, (2, n), generator=g)
+    nxt = torch.randint(0, 320, (), generator=g)
+    # capacity 12: the pool doubles while the workers decode; stock: the prompt
+    # cache comes from transformers' own forward
+    for capacity, stock in ((None, None), (12, None), (None, model)):
+        outs, pre, w0, w1 = reference_caller(ours, OracleOps, prompt, own, nxt, capacity, stock)
+        for w in range(2):
+            ref = ref_logits(model, torch.cat([prompt, own[w]]))
+            for i in range(n):
+                assert torch.allclose(outs[i][w, -1], ref[P + i], atol=1e-4, rtol=1e-4), (capacity, stock, w, i)
+        assert w0.get_seq_length() == n and w1.get_seq_length() == n and pre.get_seq_length() == P + n
+        with torch.no_grad():
+            full = model(input_ids=torch.cat([prompt, own[0]])[None], use_cache=True).past_key_values
+        for layer in range(2):
+            assert torch.allclose(pre.layers[layer].keys, full.layers[layer].keys, atol=1e-5, rtol=1e-5)
+            assert torch.allclose(pre.layers[layer].values, full.layers[layer].values, atol=1e-6)
+        ref = ref_logits(model, torch.cat([prompt, own[0], nxt[None]]))
+        assert torch.allclose(outs[-1][0, -1], ref[-1], atol=1e-4, rtol=1e-4), capacity
+
+
+def test_merge_caches_plain_transformers_caches_cpu():
+    """merge_caches on two caches no DVAttnCache holds: the reference's own
+    steps (keys rotated by the target's length, then target.update).  The
+    appended keys must be those transformers computes for the source tokens at
+    positions shifted by the target's length (rotary attention depends on
+    relative positions only, so the source's hidden states are unchanged), its
+    values the source's own, and the target's tokens untouched."""
+    from dvattention_amd import hf
+    model = tiny_qwen2(torch.float32, "cpu")
+    g = torch.Generator().manual_seed(13)
+    a = torch.randint(0, 320, (7,), generator=g)
+    b = torch.randint(0, 320, (4,), generator=g)
+    with torch.no_grad():
+        ca = model(input_ids=a[None], use_cache=True).past_key_values
+        cb = model(input_ids=b[None], use_cache=True).past_key_values
+        shifted = model(input_ids=b[None], position_ids=torch.arange(7, 11)[None], use_cache=True).past_key_values
+    before = [(ca.layers[l].keys.clone(), ca.layers[l].values.clone()) for l in range(2)]
+    hf.merge_caches(ca, cb, model.model)
+    assert ca.get_seq_length() == 11
+    for layer in range(2):
+        k, v = ca.layers[layer].keys, ca.layers[layer].values
+        assert torch.equal(k[:, :, :7], before[layer][0]) and torch.equal(v[:, :, :7], before[layer][1])
+        assert torch.allclose(k[:, :, 7:], shifted.layers[layer].keys, atol=1e-4, rtol=1e-4), layer
+        assert torch.equal(v[:, :, 7:], cb.layers[layer].values)
+
+
 def test_reference_import_path_cpu():
     """``import dvattn.attention`` (the reference's module path) registers the
     operators and exposes the reference's names over this build."""
@@ -318,6 +401,38 @@ def test_eager_and_hip_modules_agree_gpu(gpu, dtype, tol):
     for x, y in zip(*results):
         err = (x - y).abs().max().item()
         assert err <= tol, err
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 5e-4), (torch.bfloat16, 6e-2)])
+def test_reference_signature_with_transformers_caches_gpu(gpu, dtype, tol):
+    """The reference's call shape on transformers DynamicCaches with the HIP
+    operators: workers against transformers on [prompt, own], then the merged
+    prompt cache against transformers' cache of the concatenated sequence and
+    the next token's logits."""
+    from dvattention_amd import hf
+    model = tiny_qwen2(dtype, gpu)
+    ours = surgery_copy(model)
+    g = torch.Generator().manual_seed(12)
+    P, n = 9, 3
+    prompt = torch.randint(0, 320, (P,), generator=g).to(gpu)
+    own = torch.randint(0, 320, (2, n), generator=g).to(gpu)
+    nxt = torch.randint(0, 320, (), generator=g).to(gpu)
+    outs, pre, w0, w1 = reference_caller(ours, hf.HipOps, prompt, own, nxt, capacity=12)
+    for w in range(2):
+        ref = ref_logits(model, torch.cat([prompt, own[w]]))
+        for i in range(n):
+            err = (outs[i][w, -1] - ref[P + i]).abs().max().item()
+            assert err <= tol, (w, i, err)
+    assert w0.get_seq_length() == n and pre.get_seq_length() == P + n
+    with torch.no_grad():
+        full = model(input_ids=torch.cat([prompt, own[0]])[None], use_cache=True).past_key_values
+    ktol = 1e-5 if dtype == torch.float32 else 3e-2
+    for layer in range(2):
+        err = (pre.layers[layer].keys.float() - full.layers[layer].keys.float()).abs().max().item()
+        assert err <= ktol * max(1.0, full.layers[layer].keys.abs().max().item()), (layer, err)
+    ref = ref_logits(model, torch.cat([prompt, own[0], nxt[None]]))
+    assert (outs[-1][0, -1] - ref[-1]).abs().max().item() <= tol
 
 
 @pytest.mark.gpu
