@@ -2,7 +2,7 @@
 """Benchmark of the MI355X DVAttn operators on the five BASELINE configurations.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,3,4,5,5v] [--no-cpu]
-    python bench.py --read-ceiling | --mfma-ceiling      (measurement probes only)
+    python bench.py --read-ceiling | --mfma-ceiling | --small-crossover      (measurement probes only)
 
 One "step" is one call of the operator over one batch of synthetic, seeded
 inputs already resident in HBM.  The headline line (``value``) is configuration
@@ -265,6 +265,83 @@ def mfma_ceiling(device, iters: int = 2000, calls: int = 10) -> dict:
     return {"cus": cus, "iters": iters, "rows": rows}
 
 
+# Calls of the crossover table: (W, Hkv, fragment lengths); the query of each
+# sequence sits after its views and sees every key.
+CROSSOVER_CALLS = [(1, 1, [512]), (1, 8, [512]), (1, 1, [4096]), (2, 8, [256, 64]), (2, 8, [512]),
+                   (4, 8, [512]), (32, 8, [64]), (1, 8, [2048]), (8, 8, [256])]
+
+
+def small_crossover(device, min_us: float = 3000.0) -> dict:
+    """dvattn_fused through the single-launch path (DVATTN_SMALL_PATH=force)
+    and through the general path (=0) on the same calls: µs per call, back to
+    back, over enough input replicas that every call reads its K/V from HBM.
+    Its rows set the workgroup limit of the single-launch path (dv_capi.hip
+    small_path_chunks): past it the merge protocol's fences cost more than the
+    general path's three launches."""
+    from dvattention_amd import attention as A
+    from dvattention_amd import workloads as WL
+    rows = []
+    saved = os.environ.get("DVATTN_SMALL_PATH")
+    try:
+        for dtype in (torch.float32, torch.bfloat16):
+            es = 4 if dtype == torch.float32 else 2
+            for W, Hkv, lens in CROSSOVER_CALLS:
+                Hq, E, R, F = 16 * Hkv, 128, 64, len(lens)
+                kv = W * Hkv * sum(lens) * 2 * E * es
+                nrep = replicas_for(kv, max_replicas=2048)
+                gen = torch.Generator(device=device).manual_seed(7)
+                pos = sum(lens)
+                loc = torch.tensor([[[pos - sum(lens[:f])]] * W for f in range(F)], dtype=torch.int32, device=device)
+                c, s_ = WL.hf_cos_sin(loc.cpu().numpy(), R, 1e4)
+                c, s_ = c.to(device), s_.to(device)
+                fl = torch.tensor(lens, dtype=torch.int32, device=device)
+                reps = []
+                for _ in range(nrep):
+                    q = torch.randn(W, Hq, 1, E, generator=gen, device=device).to(dtype)
+                    ks = [torch.randn(W, Hkv, L, E, generator=gen, device=device).to(dtype) for L in lens]
+                    vs = [torch.randn(W, Hkv, L, E, generator=gen, device=device).to(dtype) for L in lens]
+                    reps.append((q, ks, vs, torch.empty(F, W, Hq, 1, E, dtype=dtype, device=device),
+                                 torch.empty(W, Hq, 1, E, dtype=dtype, device=device)))
+
+                def call(j):
+                    q, ks, vs, rq, out = reps[j % nrep]
+                    A.dvattn_fused(q, loc, ks, vs, E ** -0.5, fl, c, s_, rotated_queries=rq, out=out)
+
+                row = {"dtype": str(dtype).replace("torch.", ""), "W": W, "Hkv": Hkv, "lens": lens,
+                       "chunks": sum(-(-L // 64) for L in lens)}
+                row["workgroups"] = W * Hkv * row["chunks"]
+                for mode in ("force", "0"):
+                    os.environ["DVATTN_SMALL_PATH"] = mode
+                    for j in range(5):
+                        call(j)
+                    torch.cuda.synchronize()
+                    t = time.perf_counter()
+                    for j in range(10):
+                        call(j)
+                    torch.cuda.synchronize()
+                    est = (time.perf_counter() - t) * 1e6 / 10
+                    n = max(50, int(min_us / max(est, 1.0)))
+                    stream = torch.cuda.current_stream()
+                    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                    a.record(stream)
+                    for j in range(n):
+                        call(j)
+                    b.record(stream)
+                    torch.cuda.synchronize()
+                    row["single_us" if mode == "force" else "general_us"] = round(a.elapsed_time(b) * 1e3 / n, 2)
+                rows.append(row)
+                log(f"[bench] {row['dtype']} W={W} Hkv={Hkv} lens={lens}: {row['workgroups']} workgroups, single "
+                    f"{row['single_us']} us, general {row['general_us']} us per call")
+                del reps
+                torch.cuda.empty_cache()
+    finally:
+        if saved is None:
+            os.environ.pop("DVATTN_SMALL_PATH", None)
+        else:
+            os.environ["DVATTN_SMALL_PATH"] = saved
+    return {"rows": rows}
+
+
 def _time_calls(fn, n_inputs: int, steps: int, warmup: int) -> tuple:
     """Mean µs per call of fn(j % n_inputs): (a) `steps` eager back-to-back calls
     (HIP events; small kernels are bound by the host's launch rate there) and
@@ -440,6 +517,8 @@ def main() -> int:
                     help="only the paged-read probe on configurations 2 and 4 (one JSON line)")
     ap.add_argument("--mfma-ceiling", action="store_true",
                     help="only the MFMA rate probe, alone and with other VALU work per MFMA (one JSON line)")
+    ap.add_argument("--small-crossover", action="store_true",
+                    help="only the single-launch vs general path timings of dvattn_fused (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the operator has no multi-GPU path); "
@@ -463,6 +542,9 @@ def main() -> int:
         log(f"[bench] plain streaming read of {plain['bytes'] >> 30} GiB: {plain['nontemporal_GBs']} GB/s "
             f"non-temporal, {plain['default_GBs']} GB/s default policy")
         print(json.dumps({"read_ceiling": rows, "plain_read": plain}), flush=True)
+        return 0
+    if args.small_crossover:
+        print(json.dumps({"small_crossover": small_crossover(device)}), flush=True)
         return 0
     if args.mfma_ceiling:
         res = mfma_ceiling(device)

@@ -457,13 +457,16 @@ dvattn_status sdpa_launch(int dtype, dv::DecodeParams& p, const std::vector<dv::
 // or -1 for the general path.
 // DVATTN_SMALL_PATH (read with getenv on every call): "0" turns the path off;
 // "require" makes a call it cannot take fail with DVATTN_ERR_UNSUPPORTED
-// (*refused).  Changing the variable while other threads call into the library
-// is undefined (getenv races with setenv); set it before the first call.
+// (*refused); "force" takes it past the workgroup limit below as well (for
+// measuring that limit: bench.py --small-crossover).  Changing the variable
+// while other threads call into the library is undefined (getenv races with
+// setenv); set it before the first call.
 int small_path_chunks(int dtype, const dvattn_shape* s, const int* fragment_tokens, bool rotating, bool* refused) {
     *refused = false;
     const char* env = getenv("DVATTN_SMALL_PATH");
     if (env && env[0] == '0') return -1;
     const bool require = env && strcmp(env, "require") == 0;
+    const bool force = env && strcmp(env, "force") == 0;
     int chunks = -1;
     if (s->F >= 1 && s->F <= dv::kMaxFragArgs && (!rotating || s->rotary_dim % 8 == 0)) {
         chunks = dv::small_chunks(s->F, fragment_tokens);
@@ -476,7 +479,7 @@ int small_path_chunks(int dtype, const dvattn_shape* s, const int* fragment_toke
         // general path (rotation, decode and merge launches) is faster
         // (measured crossover about 190 workgroups for fp32, about 110 for
         // 16-bit types, whose general path is faster).
-        if (chunks > 1 && items * chunks > dv::small_max_merged(dtype)) chunks = -1;
+        if (chunks > 1 && items * chunks > dv::small_max_merged(dtype) && !force) chunks = -1;
         if (chunks >= 1 && dv::small_workspace_bytes(items, chunks) > dvattn_sdpa_workspace_size(dtype, s, -1))
             chunks = -1;
     }
