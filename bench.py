@@ -272,16 +272,17 @@ CROSSOVER_CALLS = [(1, 1, [512]), (1, 8, [512]), (1, 1, [4096]), (2, 8, [256, 64
 
 
 def small_crossover(device, min_us: float = 3000.0) -> dict:
-    """dvattn_fused through the single-launch path (DVATTN_SMALL_PATH=force)
-    and through the general path (=0) on the same calls: µs per call, back to
+    """dvattn_fused through the single-launch path (library option small_path =
+    force) and through the general path (off) on the same calls: µs per call, back to
     back, over enough input replicas that every call reads its K/V from HBM.
     Its rows set the workgroup limit of the single-launch path (dv_capi.hip
     small_path_chunks): past it the merge protocol's fences cost more than the
     general path's three launches."""
     from dvattention_amd import attention as A
+    from dvattention_amd import capi
     from dvattention_amd import workloads as WL
     rows = []
-    saved = os.environ.get("DVATTN_SMALL_PATH")
+    saved = capi.get_option("small_path")
     try:
         for dtype in (torch.float32, torch.bfloat16):
             es = 4 if dtype == torch.float32 else 2
@@ -310,8 +311,8 @@ def small_crossover(device, min_us: float = 3000.0) -> dict:
                 row = {"dtype": str(dtype).replace("torch.", ""), "W": W, "Hkv": Hkv, "lens": lens,
                        "chunks": sum(-(-L // 64) for L in lens)}
                 row["workgroups"] = W * Hkv * row["chunks"]
-                for mode in ("force", "0"):
-                    os.environ["DVATTN_SMALL_PATH"] = mode
+                for mode in ("force", "off"):
+                    capi.set_option("small_path", capi.SMALL_PATH[mode])
                     for j in range(5):
                         call(j)
                     torch.cuda.synchronize()
@@ -335,10 +336,7 @@ def small_crossover(device, min_us: float = 3000.0) -> dict:
                 del reps
                 torch.cuda.empty_cache()
     finally:
-        if saved is None:
-            os.environ.pop("DVATTN_SMALL_PATH", None)
-        else:
-            os.environ["DVATTN_SMALL_PATH"] = saved
+        capi.set_option("small_path", saved)
     return {"rows": rows}
 
 

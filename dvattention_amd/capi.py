@@ -23,7 +23,7 @@ STATUS = {0: "DVATTN_OK", 1: "DVATTN_ERR_INVALID", 2: "DVATTN_ERR_UNSUPPORTED", 
 
 # Every function include/dvattn_amd.h declares.
 EXPORTED = [
-    "dvattn_last_error", "dvattn_abi_version",
+    "dvattn_last_error", "dvattn_abi_version", "dvattn_set_option", "dvattn_get_option",
     "dvattn_paged_sdpa_workspace_size", "dvattn_paged_sdpa", "dvattn_paged_sdpa_noalloc",
     "dvattn_varlen_paged_sdpa_workspace_size", "dvattn_varlen_paged_sdpa",
     "dvattn_sdpa_workspace_size", "dvattn_sdpa", "dvattn_fused",
@@ -97,8 +97,25 @@ def lib() -> ctypes.CDLL:
                                              ctypes.POINTER(KvLayout), _VP]
         L.dvattn_view_metadata.restype = _I
         L.dvattn_view_metadata.argtypes = [_VP, _VP, _VP, _VP, _VP, _VP, _F, _I, _I, _I, _I, _I, _VP]
+        L.dvattn_set_option.restype = _I
+        L.dvattn_set_option.argtypes = [ctypes.c_char_p, _I]
+        L.dvattn_get_option.restype = _I
+        L.dvattn_get_option.argtypes = [ctypes.c_char_p]
         _lib = L
     return _lib
+
+
+# dvattn_set_option values of "small_path"
+SMALL_PATH = {"off": 0, "auto": 1, "require": 2, "force": 3}
+
+
+def set_option(name: str, value: int) -> None:
+    """Process-wide switch of the library (include/dvattn_amd.h: dvattn_set_option)."""
+    _check(lib().dvattn_set_option(name.encode(), int(value)))
+
+
+def get_option(name: str) -> int:
+    return lib().dvattn_get_option(name.encode())
 
 
 def dtype_code(dt: torch.dtype) -> int:

@@ -7,6 +7,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <initializer_list>
 #include <mutex>
 #include <vector>
@@ -142,9 +143,71 @@ size_t contig_table_bytes(int F) {
 
 }  // namespace
 
+namespace dv {
+
+namespace {
+
+// Option values; kUnset until first read (then from the environment).
+constexpr int kUnset = -1;
+std::atomic<int> g_options[kOptCount] = {kUnset};
+
+int option_from_env(Option) {
+    const char* e = getenv("DVATTN_SMALL_PATH");
+    if (!e) return kSmallAuto;
+    if (e[0] == '0') return kSmallOff;
+    if (strcmp(e, "require") == 0) return kSmallRequire;
+    if (strcmp(e, "force") == 0) return kSmallForce;
+    return kSmallAuto;
+}
+
+}  // namespace
+
+int option(Option o) {
+    int v = g_options[o].load(std::memory_order_relaxed);
+    if (v == kUnset) {
+        int expected = kUnset;
+        const int init = option_from_env(o);
+        g_options[o].compare_exchange_strong(expected, init, std::memory_order_relaxed);
+        v = g_options[o].load(std::memory_order_relaxed);
+    }
+    return v;
+}
+
+void set_option(Option o, int value) { g_options[o].store(value, std::memory_order_relaxed); }
+
+// splitmix64 of a process-wide call counter, 48 bits, nonzero
+unsigned long long next_call_tag() {
+    static std::atomic<unsigned long long> calls{0x5eed5eedull};
+    unsigned long long z = calls.fetch_add(0x9e3779b97f4a7c15ull, std::memory_order_relaxed);
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    z ^= z >> 31;
+    z &= (1ull << 48) - 1ull;
+    return z ? z : 1ull;
+}
+
+}  // namespace dv
+
 extern "C" {
 
 const char* dvattn_last_error(void) { return g_err; }
+
+dvattn_status dvattn_set_option(const char* name, int value) {
+    if (!name) return fail(DVATTN_ERR_INVALID, "dvattn_set_option: null name");
+    if (strcmp(name, "small_path") == 0) {
+        if (value < dv::kSmallOff || value > dv::kSmallForce)
+            return fail(DVATTN_ERR_INVALID, "small_path: 0 (off), 1 (auto), 2 (require) or 3 (force), not %d", value);
+        dv::set_option(dv::kOptSmallPath, value);
+        return ok();
+    }
+    return fail(DVATTN_ERR_INVALID, "unknown option \"%s\" (small_path)", name);
+}
+
+int dvattn_get_option(const char* name) {
+    if (!name) return -1;
+    if (strcmp(name, "small_path") == 0) return dv::option(dv::kOptSmallPath);
+    return -1;
+}
 
 int dvattn_abi_version(void) { return DVATTN_ABI_VERSION; }
 
@@ -455,18 +518,16 @@ dvattn_status sdpa_launch(int dtype, dv::DecodeParams& p, const std::vector<dv::
 // (so the choice depends on the shape and the fragment lengths only); rotating
 // calls (dvattn_fused) also need rotary_dim % 8 == 0.  Returns the chunk count,
 // or -1 for the general path.
-// DVATTN_SMALL_PATH (read with getenv on every call): "0" turns the path off;
-// "require" makes a call it cannot take fail with DVATTN_ERR_UNSUPPORTED
-// (*refused); "force" takes it past the workgroup limit below as well (for
-// measuring that limit: bench.py --small-crossover).  Changing the variable
-// while other threads call into the library is undefined (getenv races with
-// setenv); set it before the first call.
+// Option small_path (dvattn_set_option; DVATTN_SMALL_PATH at first use): off
+// turns the path off; require makes a call it cannot take fail with
+// DVATTN_ERR_UNSUPPORTED (*refused); force takes it past the workgroup limit
+// below as well (for measuring that limit: bench.py --small-crossover).
 int small_path_chunks(int dtype, const dvattn_shape* s, const int* fragment_tokens, bool rotating, bool* refused) {
     *refused = false;
-    const char* env = getenv("DVATTN_SMALL_PATH");
-    if (env && env[0] == '0') return -1;
-    const bool require = env && strcmp(env, "require") == 0;
-    const bool force = env && strcmp(env, "force") == 0;
+    const int mode = dv::option(dv::kOptSmallPath);
+    if (mode == dv::kSmallOff) return -1;
+    const bool require = mode == dv::kSmallRequire;
+    const bool force = mode == dv::kSmallForce;
     int chunks = -1;
     if (s->F >= 1 && s->F <= dv::kMaxFragArgs && (!rotating || s->rotary_dim % 8 == 0)) {
         chunks = dv::small_chunks(s->F, fragment_tokens);

@@ -708,11 +708,8 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
             }
         } else {
             const int tb = wv * kTiles + t;  // token within the block
-            float* sbase = p.part + (long long)slot * p.slot_floats;
-            float* o = sbase + (tb * kGqa + n) * kHeadDim;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(o + c * 16 + g * 4) = tl[t].o[c] * inv;
-            if (g == 0) sbase[kTokBlk * kGqa * kHeadDim + tb * kGqa + n] = lt > 0.0f ? tl[t].m + log2f(lt) : -DV_INF;
+            store_partial<DT>(p.part + (long long)slot * p.slot_floats, kTokBlk * kGqa, tb * kGqa + n, g, tl[t].o,
+                              inv, lt > 0.0f ? tl[t].m + log2f(lt) : -DV_INF);
         }
     }
     }
@@ -752,52 +749,12 @@ __global__ __launch_bounds__(256) void dv_merge_chunk(const DecodeParams p) {
     if (tb >= gr.ntok) return;
     const int tid = threadIdx.x;
     const int n = tid >> 4;
-    const int d = (tid & 15) * 8;
+    const int d[1] = {(tid & 15) * 8};
     const int h = hkv * kGqa + n;
-    raw* o = reinterpret_cast<raw*>(p.out) + out_row<RM>(p, gr, tb, h) + d;
-    const int j = tb * kGqa + n;
-    const int lse_off = kTokBlk * kGqa * kHeadDim + j;
-    const int val_off = j * kHeadDim + d;
-    float m = -DV_INF, wsum = 0.0f;
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    constexpr int kB = 8;
-    for (int k0 = 0; k0 < cnt; k0 += kB) {
-        float lse[kB];
-        f32x4 v0[kB], v1[kB];
-#pragma unroll
-        for (int i = 0; i < kB; ++i) {
-            const bool in = k0 + i < cnt;
-            const float* sp = p.part + (long long)(base + (in ? k0 + i : k0)) * p.slot_floats;
-            lse[i] = in ? sp[lse_off] : -DV_INF;
-            v0[i] = ld16f(sp + val_off);
-            v1[i] = ld16f(sp + val_off + 4);
-        }
-        float bm = m;
-#pragma unroll
-        for (int i = 0; i < kB; ++i) bm = fmaxf(bm, lse[i]);
-        if (bm == -DV_INF) continue;
-        const float sc = exp2f(m - bm);
-        wsum *= sc;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] *= sc;
-#pragma unroll
-        for (int i = 0; i < kB; ++i) {
-            const float wgt = exp2f(lse[i] - bm);
-            wsum += wgt;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc[e] += wgt * v0[i][e];
-                acc[4 + e] += wgt * v1[i][e];
-            }
-        }
-        m = bm;
-    }
-    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
-    const u32x4 pk = {pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv),
-                      pack2<DT>(acc[4] * inv, acc[5] * inv), pack2<DT>(acc[6] * inv, acc[7] * inv)};
-    *reinterpret_cast<u32x4*>(o) = pk;
+    raw* o = reinterpret_cast<raw*>(p.out) + out_row<RM>(p, gr, tb, h) + d[0];
+    float v[1][8];
+    merge_runs<DT, 1>(p.part, p.slot_floats, kTokBlk * kGqa, tb * kGqa + n, d, base, cnt, v);
+    store_run8<DT>(o, v[0]);
 }
 
 size_t lds_bytes(int nrows) {

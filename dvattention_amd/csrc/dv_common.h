@@ -52,7 +52,7 @@ struct FragDesc {
 
 struct DecodeParams {
     void* out;
-    float* part;          // partial results, slot-major: [slot][hpw*16][Ev] then [slot][hpw*16] lse
+    float* part;          // partial results, slot-major (layout: store_partial in dv_device.h)
     int* dir;             // per (row, head-group) segment: {first slot, piece count}
     const int* loc;
     const void* q;
@@ -162,6 +162,18 @@ inline hipError_t once_per_device(std::atomic<unsigned long long>& done, int dev
     if (e == hipSuccess) done.fetch_or(bit, std::memory_order_release);
     return e;
 }
+
+// Process-wide switches (dvattn_set_option): each starts from its environment
+// variable, read once at first use, and a call of dvattn_set_option replaces it.
+//   kOptSmallPath  (DVATTN_SMALL_PATH: "0" off, "require", "force"; default auto)
+enum Option : int { kOptSmallPath = 0, kOptCount = 1 };
+enum SmallPathMode : int { kSmallOff = 0, kSmallAuto = 1, kSmallRequire = 2, kSmallForce = 3 };
+int option(Option o);
+void set_option(Option o, int value);
+
+// Per-call tags for arrival flags: 48 bits, nonzero, distinct for consecutive
+// calls of the process.
+unsigned long long next_call_tag();
 
 // A per-mille tuning value from the environment, clamped to [0, 200].
 inline int env_per_mille(const char* name, int dflt) {

@@ -269,13 +269,8 @@ __device__ void process_piece(const DecodeParams& p, unsigned char* vt, int row,
             }
         }
     } else {
-        float* sbase = p.part + (long long)slot * p.slot_floats;
-        float* o = sbase + (wv * kGqa + n) * kHeadDim;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(o + c * 16 + g * 4) = st.o[c] * inv;
-        if (g == 0) {
-            sbase[p.hpw * kGqa * kHeadDim + wv * kGqa + n] = lt > 0.0f ? st.m + log2f(lt) : -DV_INF;
-        }
+        store_partial<DT>(p.part + (long long)slot * p.slot_floats, p.hpw * kGqa, wv * kGqa + n, g, st.o, inv,
+                          lt > 0.0f ? st.m + log2f(lt) : -DV_INF);
     }
 }
 
@@ -310,6 +305,15 @@ __global__ __launch_bounds__(256) void dv_decode(const DecodeParams p) {
 // conflicts.  Completion is tracked with explicit vmcnt waits (16 loads per
 // stage and wave); the physical pages of the current key range sit in a
 // per-wave LDS page cache, so the loop issues no other vector-memory operation.
+
+// Output row of query head h of decode row `row` (varlen rows: packed tokens).
+template <int DT, int RM>
+__device__ inline typename Tr<DT>::raw* out_row_ptr(const DecodeParams& p, int row, int h) {
+    using raw = typename Tr<DT>::raw;
+    if (RM == kRowVarlen) return reinterpret_cast<raw*>(p.out) + ((long long)row * p.Hq + h) * kHeadDim;
+    const int w = row / p.S, s = row - (row / p.S) * p.S;
+    return reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+}
 
 namespace stream {
 
@@ -652,11 +656,8 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
             *reinterpret_cast<u32x2*>(o + c * 16 + g * 4) = pk;
         }
     } else {
-        float* sbase = p.part + (long long)slot * p.slot_floats;
-        float* o = sbase + (wv * kGqa + n) * kHeadDim;
-#pragma unroll
-        for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(o + c * 16 + g * 4) = st.o[c] * inv;
-        if (g == 0) sbase[p.hpw * kGqa * kHeadDim + wv * kGqa + n] = lt > 0.0f ? st.m + log2f(lt) : -DV_INF;
+        store_partial<DT>(p.part + (long long)slot * p.slot_floats, p.hpw * kGqa, wv * kGqa + n, g, st.o, inv,
+                          lt > 0.0f ? st.m + log2f(lt) : -DV_INF);
     }
 }
 
@@ -678,20 +679,17 @@ __global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
 
 // ---- split merge -------------------------------------------------------------------
 
-constexpr int kMergeBatch = 8;  // pieces whose loads are in flight together
-
 // Block (segment, KV head, quarter of the head dims) with one wave: thread t
 // handles query head t/4, dims [q*32 + (t%4)*8, +8).  count == 1: already final;
 // count == 0: no visible key -> zeros (paged_kernel_v21.cuh:318); otherwise the
-// base-2-LSE-weighted sum of the pieces' normalised outputs
-// (paged_kernel_v21.cuh:325-364).  The quarters spread a long segment's
-// partials (up to ~40 pieces x 8 KiB per KV head) over four CUs: one CU reads
-// at only ~50-100 GB/s, which set the merge time of segments with many pieces.
+// base-2-LSE-weighted sum of the pieces' normalised outputs (merge_runs,
+// paged_kernel_v21.cuh:325-364).  The quarters spread a long segment's partials
+// (up to ~40 pieces x 8 KiB per KV head) over four CUs: one CU reads at only
+// ~50-100 GB/s, which set the merge time of segments with many pieces.
 constexpr int kMergeQuarters = 4;
 
 template <int DT, int RM>
 __global__ __launch_bounds__(64) void dv_merge(const DecodeParams p) {
-    using raw = typename Tr<DT>::raw;
     const int qi = blockIdx.x % kMergeQuarters;
     const int sw = blockIdx.x / kMergeQuarters;
     const int sg = sw / p.hpw;
@@ -699,66 +697,12 @@ __global__ __launch_bounds__(64) void dv_merge(const DecodeParams p) {
     const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
     if (cnt == 1) return;
     const int NHG = p.Hkv / p.hpw;
-    const int tid = threadIdx.x;
-    const int n = tid >> 2;
-    const int d = qi * 32 + (tid & 3) * 8;
+    const int n = threadIdx.x >> 2;
     const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
-    const int row = p.row_begin + r;
-    const int h = (hg * p.hpw + wi) * kGqa + n;
-    raw* o;
-    if (RM == kRowVarlen) {
-        o = reinterpret_cast<raw*>(p.out) + ((long long)row * p.Hq + h) * kHeadDim + d;
-    } else {
-        const int w = row / p.S, s = row - (row / p.S) * p.S;
-        o = reinterpret_cast<raw*>(p.out) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim + d;
-    }
-    const int j = wi * kGqa + n;
-    const int lse_off = p.hpw * kGqa * kHeadDim + j;
-    const int val_off = j * kHeadDim + d;
-    float m = -DV_INF, wsum = 0.0f;
-    float acc[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    for (int k0 = 0; k0 < cnt; k0 += kMergeBatch) {
-        float lse[kMergeBatch];
-        f32x4 v0[kMergeBatch], v1[kMergeBatch];
-#pragma unroll
-        for (int i = 0; i < kMergeBatch; ++i) {
-            const bool in = k0 + i < cnt;
-            const float* sp = p.part + (long long)(base + (in ? k0 + i : k0)) * p.slot_floats;
-            lse[i] = in ? sp[lse_off] : -DV_INF;
-            v0[i] = ld16f(sp + val_off);
-            v1[i] = ld16f(sp + val_off + 4);
-        }
-        float bm = m;
-#pragma unroll
-        for (int i = 0; i < kMergeBatch; ++i) bm = fmaxf(bm, lse[i]);
-        if (bm == -DV_INF) continue;
-        const float sc = exp2f(m - bm);  // m == -inf -> 0
-        wsum *= sc;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] *= sc;
-#pragma unroll
-        for (int i = 0; i < kMergeBatch; ++i) {
-            const float wgt = exp2f(lse[i] - bm);  // empty piece (-inf) -> 0
-            wsum += wgt;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc[e] += wgt * v0[i][e];
-                acc[4 + e] += wgt * v1[i][e];
-            }
-        }
-        m = bm;
-    }
-    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
-    if constexpr (DT == kF32) {
-        *reinterpret_cast<f32x4*>(o) = f32x4{acc[0] * inv, acc[1] * inv, acc[2] * inv, acc[3] * inv};
-        *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4] * inv, acc[5] * inv, acc[6] * inv, acc[7] * inv};
-    } else {
-        const u32x4 pk = {pack2<DT>(acc[0] * inv, acc[1] * inv), pack2<DT>(acc[2] * inv, acc[3] * inv),
-                          pack2<DT>(acc[4] * inv, acc[5] * inv), pack2<DT>(acc[6] * inv, acc[7] * inv)};
-        *reinterpret_cast<u32x4*>(o) = pk;
-    }
+    const int d[1] = {qi * 32 + (int)(threadIdx.x & 3) * 8};
+    float v[1][8];
+    merge_runs<DT, 1>(p.part, p.slot_floats, p.hpw * kGqa, wi * kGqa + n, d, base, cnt, v);
+    store_run8<DT>(out_row_ptr<DT, RM>(p, p.row_begin + r, (hg * p.hpw + wi) * kGqa + n) + d[0], v[0]);
 }
 
 // ---- host side --------------------------------------------------------------------
@@ -858,6 +802,10 @@ hipError_t dispatch_modes(int qmode, int kvmode, int rowmode, const DecodeParams
 
 const char* last_hip_site() { return g_site; }
 
+// Workspace per segment after the partial slots: merge directory {first slot,
+// pieces}.
+constexpr int kSegBytes = 8;
+
 size_t decode_workspace_bytes(int nrows_total, int Hkv, int device, int dtype) {
     (void)dtype;
     if (nrows_total <= 0 || Hkv <= 0) return 0;
@@ -870,7 +818,7 @@ size_t decode_workspace_bytes(int nrows_total, int Hkv, int device, int dtype) {
     const long long slots = nwg + nseg;
     size_t bytes = (size_t)(slots * slot_floats * 4);
     bytes = (bytes + 255) & ~(size_t)255;
-    bytes += (size_t)(nseg * 2 * 4);
+    bytes += (size_t)(nseg * kSegBytes);
     return bytes;
 }
 
@@ -891,9 +839,11 @@ hipError_t launch_decode(int dtype, int qmode, int kvmode, int rowmode, const De
     const long long slots_cap = max_wg + (long long)rows_cap * nhg;
     size_t part_bytes = (size_t)(slots_cap * p.slot_floats * 4);
     part_bytes = (part_bytes + 255) & ~(size_t)255;
-    if (ws_bytes < part_bytes + (size_t)rows_cap * nhg * 2 * 4) return hipErrorInvalidValue;
-    p.part = reinterpret_cast<float*>(workspace);
-    p.dir = reinterpret_cast<int*>(reinterpret_cast<unsigned char*>(workspace) + part_bytes);
+    const long long nseg_cap = (long long)rows_cap * nhg;
+    if (ws_bytes < part_bytes + (size_t)nseg_cap * kSegBytes) return hipErrorInvalidValue;
+    unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+    p.part = reinterpret_cast<float*>(ws);
+    p.dir = reinterpret_cast<int*>(ws + part_bytes);
     p.piece_cost = dtype == kF32 ? 0 : kPieceCost;
     // the fp32 kernel waits for each 32-key stage before the next: one stage per
     // workgroup is worth it on small problems

@@ -373,4 +373,165 @@ __device__ inline void rotate_run(const typename Tr<DT>::raw* __restrict__ qrow,
     }
 }
 
+// ---- split partials -----------------------------------------------------------
+//
+// A partial slot holds, for each of its nrows query rows (row j of the slot:
+// one query head of one KV head or token), the piece's normalised output and
+// its base-2 log-sum-exp:
+//   fp32 and fp16 calls: values float[nrows][kHeadDim], lse float[nrows] after them;
+//   bf16 calls: values fp16[nrows][kHeadDim] scaled per row by 2^k, the
+//   exponents k int[nrows] right after the fp16 values, lse at the same float
+//   offset as above (the slot keeps its fp32 size; half of it is left unused).
+// The scale puts a row's largest finite magnitude in [2^14, 2^15), so every
+// stored value is within 2^-11 of that magnitude of the exact normalised
+// output: a quarter of the relative rounding (2^-9) the piece already applied
+// to the probabilities when it packed them to bf16 for P V, and 1/16 of the
+// output's own bf16 rounding.  Infinite values stay infinite, NaN stays NaN.
+// Half the bytes of fp32 partials are written and read again by the merge.
+template <int DT> constexpr bool kHalfPartials = DT == kBF16;
+
+// Scale exponent of a row whose largest finite |value| is amax (0 for an empty
+// or zero row): amax * 2^k in [2^14, 2^15), at most 2^100 so that the factor
+// stays finite for rows of tiny values.
+__device__ inline int partial_exp(float amax) {
+    const int k = 15 - __builtin_amdgcn_frexp_expf(amax);  // amax = m * 2^e, m in [0.5, 1)
+    return k < 100 ? k : 100;
+}
+
+// Lane (g, n) holds dims c*16 + g*4 + e (c < 8, e < 4) of slot row j in o
+// (unnormalised; inv = 1 / row sum); the four lanes of a row are n + 16g, and
+// every lane of the wave takes part (cross-lane maximum).  g == 0 also writes
+// the row's lse.
+template <int DT>
+__device__ inline void store_partial(float* sbase, int nrows, int j, int g, const f32x4 (&o)[8], float inv,
+                                     float lse) {
+    if constexpr (kHalfPartials<DT>) {
+        float amax = 0.0f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float a = __builtin_fabsf(o[c][e]);
+                amax = fmaxf(amax, a < DV_INF ? a : 0.0f);
+            }
+        }
+        const int k = partial_exp(rows4_max(amax) * inv);
+        const float sc = __builtin_amdgcn_ldexpf(inv, k);
+        uint16_t* h = reinterpret_cast<uint16_t*>(sbase) + j * kHeadDim;
+#pragma unroll
+        for (int c = 0; c < 8; ++c)
+            *reinterpret_cast<u32x2*>(h + c * 16 + g * 4) =
+                u32x2{pack2<kF16>(o[c][0] * sc, o[c][1] * sc), pack2<kF16>(o[c][2] * sc, o[c][3] * sc)};
+        if (g == 0) {
+            reinterpret_cast<int*>(sbase)[nrows * (kHeadDim / 2) + j] = k;
+            sbase[nrows * kHeadDim + j] = lse;
+        }
+    } else {
+        float* v = sbase + j * kHeadDim;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) *reinterpret_cast<f32x4*>(v + c * 16 + g * 4) = o[c] * inv;
+        if (g == 0) sbase[nrows * kHeadDim + j] = lse;
+    }
+}
+
+constexpr int kMergeBatch = 8;  // pieces whose loads are in flight together in a merge
+
+// Merge of the pieces [base, base + cnt) of one segment (slots of slot_floats
+// floats from part) for slot row j of nrows, NQ runs of eight dims starting at
+// d[q]: the base-2-LSE-weighted sum of the pieces' normalised outputs
+// (paged_kernel_v21.cuh:325-364), with kMergeBatch pieces' loads in flight per
+// round.  res[q][e] = merged value of dim d[q] + e; 0 when no piece has a
+// visible key.  The split-merge kernels (one run per thread) and the in-kernel
+// merge of the decode kernel (four runs per lane) share this code, so both give
+// the same bits for the same pieces.
+template <int DT, int NQ>
+__device__ inline void merge_runs(const float* part, long long slot_floats, int nrows, int j, const int (&d)[NQ],
+                                  int base, int cnt, float (&res)[NQ][8]) {
+    float m = -DV_INF, wsum = 0.0f;
+    float acc[NQ][8];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[q][e] = 0.0f;
+    for (int k0 = 0; k0 < cnt; k0 += kMergeBatch) {
+        float lse[kMergeBatch];
+        int kx[kMergeBatch];
+        u32x4 h[kMergeBatch][NQ];
+        f32x4 v0[kMergeBatch][NQ], v1[kMergeBatch][NQ];
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const bool in = k0 + i < cnt;
+            const float* sp = part + (long long)(base + (in ? k0 + i : k0)) * slot_floats;
+            lse[i] = in ? sp[nrows * kHeadDim + j] : -DV_INF;
+            if constexpr (kHalfPartials<DT>) {
+                kx[i] = reinterpret_cast<const int*>(sp)[nrows * (kHeadDim / 2) + j];
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) h[i][q] = ld16(reinterpret_cast<const uint16_t*>(sp) + j * kHeadDim + d[q]);
+            } else {
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+                    v0[i][q] = ld16f(sp + j * kHeadDim + d[q]);
+                    v1[i][q] = ld16f(sp + j * kHeadDim + d[q] + 4);
+                }
+            }
+        }
+        float bm = m;
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) bm = fmaxf(bm, lse[i]);
+        if (bm == -DV_INF) continue;
+        const float sc = exp2f(m - bm);  // m == -inf -> 0
+        wsum *= sc;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[q][e] *= sc;
+#pragma unroll
+        for (int i = 0; i < kMergeBatch; ++i) {
+            const float wgt = exp2f(lse[i] - bm);  // empty piece (-inf) -> 0
+            wsum += wgt;
+            if constexpr (kHalfPartials<DT>) {
+                const float w = __builtin_amdgcn_ldexpf(wgt, -kx[i]);
+                // halves taken by shifts: a bit cast of a vector element to
+                // f16x2 was compiled as a cast of element 0 for every element
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t hw = h[i][q][t];
+                        acc[q][2 * t] = __builtin_fmaf(w, Tr<kF16>::tof((uint16_t)(hw & 0xffffu)), acc[q][2 * t]);
+                        acc[q][2 * t + 1] = __builtin_fmaf(w, Tr<kF16>::tof((uint16_t)(hw >> 16)), acc[q][2 * t + 1]);
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        acc[q][e] = __builtin_fmaf(wgt, v0[i][q][e], acc[q][e]);
+                        acc[q][4 + e] = __builtin_fmaf(wgt, v1[i][q][e], acc[q][4 + e]);
+                    }
+                }
+            }
+        }
+        m = bm;
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) res[q][e] = acc[q][e] * inv;
+}
+
+// Eight merged values stored to the output (16-bit: one 16-byte store).
+template <int DT>
+__device__ inline void store_run8(typename Tr<DT>::raw* o, const float (&v)[8]) {
+    if constexpr (DT == kF32) {
+        *reinterpret_cast<f32x4*>(o) = f32x4{v[0], v[1], v[2], v[3]};
+        *reinterpret_cast<f32x4*>(o + 4) = f32x4{v[4], v[5], v[6], v[7]};
+    } else {
+        *reinterpret_cast<u32x4*>(o) =
+            u32x4{pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]), pack2<DT>(v[4], v[5]), pack2<DT>(v[6], v[7])};
+    }
+}
+
 }  // namespace dv

@@ -427,17 +427,6 @@ __global__ __launch_bounds__(256) void dv_small(const SmallParams sp) {
     store8<DT>(outp, acc8, wsum > 0.0f ? 1.0f / wsum : 0.0f);
 }
 
-// Per-call flag tags: splitmix64 of a process-wide call counter, 48 bits, nonzero.
-unsigned long long next_tag() {
-    static std::atomic<unsigned long long> calls{0x5eed5eedull};
-    unsigned long long z = calls.fetch_add(0x9e3779b97f4a7c15ull, std::memory_order_relaxed);
-    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-    z ^= z >> 31;
-    z &= (1ull << 48) - 1ull;
-    return z ? z : 1ull;
-}
-
 size_t align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
 }  // namespace small
@@ -473,7 +462,7 @@ hipError_t launch_small(int dtype, int qmode, SmallParams& p, void* workspace, h
     p.flags = reinterpret_cast<unsigned long long*>(workspace);
     p.part = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
                                       small::align256((size_t)items * p.chunks * sizeof(unsigned long long)));
-    p.tag = small::next_tag();
+    p.tag = next_call_tag();
     if (dtype == kF32) launch_small_dt<kF32>(qmode, p, grid, stream);
     else if (dtype == kF16) launch_small_dt<kF16>(qmode, p, grid, stream);
     else launch_small_dt<kBF16>(qmode, p, grid, stream);

@@ -111,6 +111,18 @@ typedef struct dvattn_shape {
 DVATTN_API const char* dvattn_last_error(void);
 DVATTN_API int dvattn_abi_version(void);
 
+/* Process-wide switches.  No counterpart in the reference (its kernels have no
+ * such choices).  Each starts from an environment variable, read once at first
+ * use; dvattn_set_option replaces the value for all later calls (set it while
+ * no other thread is inside a call, or those calls may see either value).
+ *   "small_path"  (DVATTN_SMALL_PATH: 0/"0" off, 1 auto = default, 2/"require",
+ *                  3/"force"): the single-launch path of dvattn_sdpa /
+ *                  dvattn_fused; require fails a call it cannot take with
+ *                  DVATTN_ERR_UNSUPPORTED, force takes it past its workgroup limit.
+ * dvattn_get_option returns the current value, -1 for an unknown name. */
+DVATTN_API dvattn_status dvattn_set_option(const char* name, int value);
+DVATTN_API int dvattn_get_option(const char* name);
+
 /* ---- paged decode attention with fused query RoPE --------------------------
  * out [W,Hq,S,Ev] T; locations [F,W,S] i32; queries [W,Hq,S,E] T;
  * cosines/sines [F,W,S,R] f32; fragment_lengths [F] i32 (device);

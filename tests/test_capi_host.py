@@ -302,3 +302,21 @@ def test_kv_append_and_metadata_null_and_empty():
     assert L.dvattn_view_metadata(p, None, p, p, p, p, 1.0, -1, 2, 3, 1, 64, None) == 1
     assert L.dvattn_view_metadata(p, p, p, p, p, p, 1.0, -1, -1, 3, 1, 64, None) == 1
     assert L.dvattn_view_metadata(None, None, None, None, None, None, 1.0, -1, 0, 3, 1, 64, None) == 0
+
+
+def test_options_set_get_and_refuse():
+    """dvattn_set_option / dvattn_get_option (host only, no GPU call)."""
+    from dvattention_amd import capi
+    before = capi.get_option("small_path")
+    assert before in capi.SMALL_PATH.values()
+    try:
+        for v in capi.SMALL_PATH.values():
+            capi.set_option("small_path", v)
+            assert capi.get_option("small_path") == v
+        with pytest.raises(capi.DvattnError):
+            capi.set_option("small_path", 9)
+        with pytest.raises(capi.DvattnError):
+            capi.set_option("no_such_option", 1)
+        assert capi.get_option("no_such_option") == -1
+    finally:
+        capi.set_option("small_path", before)

@@ -2,11 +2,11 @@
 attention and chunk merge in one kernel; dvattn_sdpa / dvattn_fused in fp32,
 fp16 and bf16).
 
-Every call here runs with DVATTN_SMALL_PATH=require, which makes a call the
-single launch cannot take fail instead of falling back, so each case is known
-to exercise it.  Outputs are checked against the CPU oracle (tolerances 1e-5
+Every call here runs with the library option small_path = require
+(dvattn_set_option), which makes a call the single launch cannot take fail
+instead of falling back, so each case is known to exercise it.  Outputs are checked against the CPU oracle (tolerances 1e-5
 fp32, 1e-3 fp16, 2e-2 bf16, as in test_gpu_parity) and against the general
-path (DVATTN_SMALL_PATH=0) on the same inputs; rotated queries bit-exactly
+path (small_path = off) on the same inputs; rotated queries bit-exactly
 against the oracle's rotation (fp32 math rounded to the storage type).
 A call whose rows have more than one chunk (one long view, or several
 views) takes the single launch only up to 160 (fp32) or 96 (16-bit)
@@ -31,8 +31,11 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.fixture
-def require_small(monkeypatch):
-    monkeypatch.setenv("DVATTN_SMALL_PATH", "require")
+def require_small():
+    from dvattention_amd import capi
+    capi.set_option("small_path", capi.SMALL_PATH["require"])
+    yield
+    capi.set_option("small_path", capi.SMALL_PATH["auto"])
 
 
 DTYPES = [torch.float32, torch.float16, torch.bfloat16]
@@ -92,7 +95,7 @@ def chunks_of(Ls):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("F,W,S,Hkv,Ls,batch,fls", CASES)
-def test_small_vs_oracle_and_general_path(dv, gpu, require_small, monkeypatch, dtype, F, W, S, Hkv, Ls, batch,
+def test_small_vs_oracle_and_general_path(dv, gpu, require_small, dtype, F, W, S, Hkv, Ls, batch,
                                           fls):
     d = make_case(F, W, S, Hkv, Ls, batch, fls, seed=F * 7 + W + S, dtype=dtype)
     chunks = chunks_of(Ls)
@@ -109,7 +112,8 @@ def test_small_vs_oracle_and_general_path(dv, gpu, require_small, monkeypatch, d
     gv = [v.to(gpu) for v in d["vals"]]
     pre = dv.dvattn_sdpa(rq_ref.to(gpu), d["loc"].to(gpu), gk, gv, 0.1, d["fl"].to(gpu))
     assert torch.equal(pre, out)  # same chunks, same merge order
-    monkeypatch.setenv("DVATTN_SMALL_PATH", "0")
+    from dvattention_amd import capi
+    capi.set_option("small_path", capi.SMALL_PATH["off"])
     gen, rq2 = run_fused(dv, d, gpu)
     assert torch.equal(rq2, rq)
     close(gen, ref, dtype, "general path")
