@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the MI355X DVAttn operators on the five BASELINE configurations.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,2u,3,4,5,5v] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--configs 1,2,2u,3,4,5,5v,5f] [--no-cpu]
     python bench.py --read-ceiling | --mfma-ceiling | --small-crossover      (measurement probes only)
 
 One "step" is one call of the operator over one batch of synthetic, seeded
@@ -15,7 +15,8 @@ step).  Every configuration is also reported under ``per_config`` (``5v``:
 configuration 5's 16-token chunks packed through the varlen op, its cross-check;
 ``2u``: configuration 2 with all 32 sequences at 8192 keys, the north star's
 "batch 32 x 8k context" read literally -- supplementary, the headline stays
-configuration 2), and the
+configuration 2; ``5f``: configuration 5's shape in fp32, the fp32 multi-query
+kernel), and the
 cache-side kernels around the path (K-side append, merge_caches re-rotation,
 view metadata) under ``cache_rows``.
 
@@ -65,7 +66,7 @@ MIN_TIMED_US = 2000.0
 
 
 def time_config(i, steps: int, warmup: int, device, exact: bool = False) -> dict:
-    """Per-call time of configuration i (1-5, "5v" or "2u").  exact: time exactly
+    """Per-call time of configuration i (1-5, "5v", "5f" or "2u").  exact: time exactly
     `steps` calls (the headline); otherwise at least `steps` calls and at least
     MIN_TIMED_US of work, estimated from the warm-up calls."""
     from dvattention_amd import workloads as WL
@@ -512,7 +513,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--configs", default="1,2,2u,3,4,5,5v")
+    ap.add_argument("--configs", default="1,2,2u,3,4,5,5v,5f")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-cache-rows", action="store_true", help="skip the K-side append / view metadata rows")
     ap.add_argument("--read-ceiling", action="store_true",
@@ -555,7 +556,7 @@ def main() -> int:
                 f"{r['clock_mhz']} MHz, {r['simd_cycles_per_mfma']} SIMD cycles per MFMA")
         print(json.dumps({"mfma_ceiling": res}), flush=True)
         return 0
-    cfgs = [x if x in ("5v", "2u") else int(x) for x in args.configs.split(",") if x]
+    cfgs = [x if x in ("5v", "2u", "5f") else int(x) for x in args.configs.split(",") if x]
     if 2 not in cfgs:
         cfgs = [2] + cfgs
     per = {}

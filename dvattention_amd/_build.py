@@ -30,7 +30,8 @@ TORCH_SO = os.path.join(HERE, "_libdvatt.so")
 # measurement-only library: the paged-read probe behind `bench.py --read-ceiling`
 PROBE_SO = os.path.join(HERE, "libdvattn_probe.so")
 
-HIP_SOURCES = ["dv_decode.hip", "dv_chunk.hip", "dv_small.hip", "dv_rope.hip", "dv_cache.hip", "dv_capi.hip"]
+HIP_SOURCES = ["dv_decode.hip", "dv_chunk.hip", "dv_chunk32.hip", "dv_small.hip", "dv_rope.hip", "dv_cache.hip",
+               "dv_capi.hip"]
 
 # gfx950 code only; packed-fp32 instructions are disabled (the host pass of
 # hipcc warns that it does not know the feature, which is harmless).

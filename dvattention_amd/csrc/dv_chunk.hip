@@ -27,33 +27,10 @@
 //  * Rows are causal-masked per token (key l visible iff l <= locations[f,w,s]).
 //  * The balanced split / LSE merge is the decode kernel's (equal key chunks per
 //    workgroup, fp32 partial slots, dv_merge_chunk).
-#include <climits>
-
-#include "dv_common.h"
-#include "dv_device.h"
-#include "dv_schedule.h"
+#include "dv_chunk.h"
 
 namespace dv {
 namespace chunk {
-
-constexpr int kWaves = 8;                     // waves per workgroup (two per SIMD)
-constexpr int kThreads = kWaves * kWave;
-constexpr int kTiles = 2;                     // 16-head query tiles (tokens) per wave
-constexpr int kHalf = kTiles / 2;             // tiles per MFMA/VALU group
-constexpr int kTokBlk = kWaves * kTiles;      // tokens per row group
-constexpr int kStages = 8;                    // K/V ring depth
-constexpr int kKvBytes = kStep * 256;         // one K (or V) stage tile: 32 keys x 256 B
-constexpr int kStageBytes = 2 * kKvBytes;     // K tile then V tile
-constexpr int kRingBytes = kStages * kStageBytes;
-constexpr int kPageCap = 2048;                // page ids cached in LDS per view sub-range
-constexpr int kAhead = 7;                     // stages in flight ahead of the one computed
-constexpr int kDmaPerStage = 2;               // per wave: 1 x K + 1 x V (1 KiB = 4 key rows each)
-
-// Start cost of a piece in the work split, in keys (query staging and rotation,
-// page ids, the ring prologue).
-constexpr int kPieceCost = 256;
-
-static __device__ __align__(16) unsigned char zrow[512];
 
 // Workgroup barrier that is also a compiler memory and scheduling barrier: no
 // LDS access or MFMA moves across it.
@@ -66,45 +43,6 @@ __device__ inline void wg_barrier() {
 // swizzled 16-byte piece positions inside a 256-byte key row
 __device__ inline int swz_k(int key, int piece) { return piece ^ (key & 15); }
 __device__ inline int swz_v(int key, int piece) { return piece ^ ((key & 7) << 1); }
-
-struct Range {
-    const unsigned char* k;  // K base (paged cache or this view's fragment)
-    const unsigned char* v;
-    long long off;           // paged: logical position of the view's key 0
-    long long bstride;       // contig: element offset of the sequence's batch entry
-    int L;                   // contig: tokens in the fragment tensor
-    uint32_t lp0;            // paged: first cached logical page
-    bool pages_ok;           // paged: every page of the current sub-range is valid
-    int w, hkv;
-    int b;                   // end (exclusive) of the view-local key range
-};
-
-// Byte offset of key l's K (= V) row, or -1 when not visible / not addressable.
-// Paged rows are indexed in 32 bits (the C ABI rejects caches of 2^32 rows or
-// more) and positions are 32-bit as in the reference (paged_kernel_v21.cuh:103-104).
-template <int KVM, bool P2>
-__device__ inline long long row_of(const DecodeParams& p, const Range& r, const int* pages, int l) {
-    if (KVM == kKvPaged) {
-        const uint32_t pos = (uint32_t)(r.off + l);
-        uint32_t lp, rr;
-        if (P2) {  // block_size a power of two
-            lp = pos >> p.bs_shift;
-            rr = pos & ((1u << p.bs_shift) - 1u);
-        } else {
-            lp = pos / (uint32_t)p.bs;
-            rr = pos - lp * (uint32_t)p.bs;
-        }
-        // the page-cache read is unconditional (clamped index), so no branch
-        // forms around it
-        const uint32_t idx = lp - r.lp0;
-        const int pg = pages[idx < (uint32_t)kPageCap ? idx : (uint32_t)(kPageCap - 1)];
-        const bool ok = l < r.b && idx < (uint32_t)kPageCap && pg >= 0;
-        const uint32_t rowidx = ((uint32_t)pg * (uint32_t)p.bs + rr) * (uint32_t)p.Hkv + (uint32_t)r.hkv;
-        return ok ? (long long)((unsigned long long)rowidx << 8) : -1;
-    } else {
-        return l < r.b ? (r.bstride + ((long long)r.hkv * r.L + l) * kHeadDim) * 2 : -1;
-    }
-}
 
 // Issue this wave's eighth of stage `st` (keys [kb0, kb0+32) of the range): key
 // rows 4*wave .. 4*wave+3 of K and of V, lane -> (row lane/16, 16-byte piece).
@@ -145,55 +83,6 @@ struct Tile {
     // updated only where m changes (sm_raise), not recomputed per stage
     float nm;
 };
-
-// A row group: up to kTokBlk query tokens of one sequence that share one K/V
-// stream.  kRowWS: group rg is block rg % nsb of sequence rg / nsb in the
-// [W, S] token grid (tokens s0 .. s0 + ntok - 1); kRowVarlen: entry rg of the
-// table dv_varlen_groups writes (packed tokens lin .. lin + ntok - 1 of
-// sequence w).  lin: the first token's index on the token axis of locations
-// and cos/sin (w * S + s0, or the packed token).
-struct Grp {
-    int w, s0, lin, ntok;
-};
-
-template <int RM>
-__device__ inline Grp group_of(const DecodeParams& p, int rg) {
-    Grp g;
-    if (RM == kRowVarlen) {
-        const int4 e = reinterpret_cast<const int4*>(p.vgroups)[rg];
-        g.lin = e.x;
-        g.ntok = e.y;
-        g.w = e.z;
-        g.s0 = 0;
-    } else {
-        const int nsb = (p.S + kTokBlk - 1) / kTokBlk;
-        g.w = rg / nsb;
-        g.s0 = (rg - g.w * nsb) * kTokBlk;
-        g.ntok = p.S - g.s0 < kTokBlk ? p.S - g.s0 : kTokBlk;
-        g.lin = g.w * p.S + g.s0;
-    }
-    return g;
-}
-
-// Length of the token axis of locations [F, tokens] and cos/sin.
-template <int RM>
-__device__ inline long long tok_axis(const DecodeParams& p) {
-    return RM == kRowVarlen ? (long long)p.T : (long long)p.W * p.S;
-}
-
-// Element offset of the query row (head h) and of the output row of token i
-// of group g (view f for pre-rotated queries [F, W, Hq, S, E]).
-template <int QM, int RM>
-__device__ inline long long q_row(const DecodeParams& p, const Grp& g, int i, int h, int f) {
-    if (RM == kRowVarlen) return ((long long)(g.lin + i) * p.Hq + h) * kHeadDim;
-    if (QM == kQPre) return ((((long long)f * p.W + g.w) * p.Hq + h) * p.S + g.s0 + i) * kHeadDim;
-    return (((long long)g.w * p.Hq + h) * p.S + g.s0 + i) * kHeadDim;
-}
-template <int RM>
-__device__ inline long long out_row(const DecodeParams& p, const Grp& g, int i, int h) {
-    if (RM == kRowVarlen) return ((long long)(g.lin + i) * p.Hq + h) * kHeadDim;
-    return (((long long)g.w * p.Hq + h) * p.S + g.s0 + i) * kHeadDim;
-}
 
 // Query tiles of this wave's tokens tok0 .. tok0 + ntile - 1 of group gr for
 // view f, staged through LDS (the K/V ring is idle between view ranges): raw
@@ -284,45 +173,7 @@ __device__ inline void stage_q_tiles(const DecodeParams& p, unsigned char* qreg,
     compiler_fence();
 }
 
-template <int KVM>
-__device__ inline const FragDesc& frag(const DecodeParams& p, int f) {
-    return f < kMaxFragArgs ? p.frags[f] : p.frag_tab[f];
-}
-
-template <int KVM>
-__device__ inline int view_vis(const DecodeParams& p, int f, int locv) {
-    long long L = p.fl[f];
-    if (KVM == kKvContig) L = L < frag<KVM>(p, f).L ? L : frag<KVM>(p, f).L;
-    long long v = (long long)locv + 1;
-    v = v < L ? v : L;
-    return v > 0 ? (int)v : 0;
-}
-
-// Location of token i of group g in view f (locations [F, tokens]).
-template <int RM>
-__device__ inline int loc_of(const DecodeParams& p, int f, const Grp& g, int i) {
-    return p.loc[(long long)f * tok_axis<RM>(p) + g.lin + i];
-}
-
-// Length of a row group's key space: per view, the union (max) over its tokens
-// of the view's visible count, summed over views -- the coordinates chunk_piece
-// walks (view f's keys follow the longest range of views 0 .. f-1).  The max
-// over tokens of the per-token sum is shorter whenever different tokens see
-// most in different views, and would leave the tail of the key space unassigned.
-template <int KVM, int RM>
-__device__ inline long long group_visible(const DecodeParams& p, int rg) {
-    const Grp g = group_of<RM>(p, rg);
-    long long total = 0;
-    for (int f = 0; f < p.F; ++f) {
-        int best = 0;
-        for (int i = 0; i < g.ntok; ++i) {
-            const int v = view_vis<KVM>(p, f, loc_of<RM>(p, f, g, i));
-            best = v > best ? v : best;
-        }
-        total += best;
-    }
-    return total;
-}
+// frag / view_vis: the views' tensors and visible key counts (dv_stream.h)
 
 // K operand of one stage (A of S^T = K Q^T): lo[cc] holds key n, hi[cc] key
 // 16 + n, dims cc*32 + g*8 .. +8 (lane (g, n)).  The K swizzle only flips
@@ -413,11 +264,6 @@ __device__ inline void mask_scores(f32x4& s0, f32x4& s1, uint32_t mask) {
         s0[i] = ((mg >> i) & 1u) ? s0[i] : -DV_INF;
         s1[i] = ((mg >> (16 + i)) & 1u) ? s1[i] : -DV_INF;
     }
-}
-
-__device__ inline uint32_t token_mask(int vis, int kb0) {
-    const int lim = vis - kb0;
-    return lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));
 }
 
 // Online softmax of two tiles over one 32-key stage, in two straight-line
@@ -734,29 +580,6 @@ __global__ __launch_bounds__(kThreads) void dv_chunk(const DecodeParams p) {
                  });
 }
 
-// Block (segment, token of the block): thread t -> head t/16, dims [(t%16)*8, +8).
-// A segment without pieces (no visible key) writes zeros, as the decode merge does.
-template <int DT, int RM>
-__global__ __launch_bounds__(256) void dv_merge_chunk(const DecodeParams p) {
-    using raw = typename Tr<DT>::raw;
-    const int sg = blockIdx.x / kTokBlk;
-    const int tb = blockIdx.x - sg * kTokBlk;
-    const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
-    if (cnt == 1) return;
-    const int NHG = p.Hkv;
-    const int r = sg / NHG, hkv = sg - (sg / NHG) * NHG;
-    const Grp gr = group_of<RM>(p, p.row_begin + r);
-    if (tb >= gr.ntok) return;
-    const int tid = threadIdx.x;
-    const int n = tid >> 4;
-    const int d[1] = {(tid & 15) * 8};
-    const int h = hkv * kGqa + n;
-    raw* o = reinterpret_cast<raw*>(p.out) + out_row<RM>(p, gr, tb, h) + d[0];
-    float v[1][8];
-    merge_runs<DT, 1>(p.part, p.slot_floats, kTokBlk * kGqa, tb * kGqa + n, d, base, cnt, v);
-    store_run8<DT>(o, v[0]);
-}
-
 size_t lds_bytes(int nrows) {
     return 256 + (size_t)kRingBytes + (size_t)kPageCap * 4 + (size_t)(kWaves + nrows + 1) * sizeof(long long);
 }
@@ -878,9 +701,13 @@ hipError_t launch1(DecodeParams p, int device, int cus, long long cap, hipStream
 
 template <int DT, int QM, int KVM, int RM>
 hipError_t launch(DecodeParams p, int device, int cus, long long cap, hipStream_t stream) {
-    if constexpr (KVM == kKvPaged)
-        if (p.bs_shift >= 0) return launch1<DT, QM, KVM, true, RM>(p, device, cus, cap, stream);
-    return launch1<DT, QM, KVM, false, RM>(p, device, cus, cap, stream);
+    if constexpr (DT == kF32) {
+        return launch_chunk32(QM, KVM, RM, p, device, cus, cap, stream);
+    } else {
+        if constexpr (KVM == kKvPaged)
+            if (p.bs_shift >= 0) return launch1<DT, QM, KVM, true, RM>(p, device, cus, cap, stream);
+        return launch1<DT, QM, KVM, false, RM>(p, device, cus, cap, stream);
+    }
 }
 
 }  // namespace chunk
@@ -934,6 +761,8 @@ hipError_t launch_groups(int dtype, int qmode, int kvmode, DecodeParams p, long 
                 e = chunk::launch<kBF16, kQRotHalf, kKvPaged, RM>(p, device, cus, cap, stream);
             else if (dtype == kF16 && qmode == kQRotHalf && kvmode == kKvPaged)
                 e = chunk::launch<kF16, kQRotHalf, kKvPaged, RM>(p, device, cus, cap, stream);
+            else if (dtype == kF32 && qmode == kQRotHalf && kvmode == kKvPaged)
+                e = chunk::launch<kF32, kQRotHalf, kKvPaged, RM>(p, device, cus, cap, stream);
             else
                 e = hipErrorInvalidValue;
         } else {
@@ -945,6 +774,10 @@ hipError_t launch_groups(int dtype, int qmode, int kvmode, DecodeParams p, long 
                 e = chunk::launch<kBF16, kQPre, kKvContig, RM>(p, device, cus, cap, stream);
             else if (dtype == kF16 && qmode == kQPre && kvmode == kKvContig)
                 e = chunk::launch<kF16, kQPre, kKvContig, RM>(p, device, cus, cap, stream);
+            else if (dtype == kF32 && qmode == kQRotFull && kvmode == kKvPaged)
+                e = chunk::launch<kF32, kQRotFull, kKvPaged, RM>(p, device, cus, cap, stream);
+            else if (dtype == kF32 && qmode == kQPre && kvmode == kKvContig)
+                e = chunk::launch<kF32, kQPre, kKvContig, RM>(p, device, cus, cap, stream);
             else
                 e = hipErrorInvalidValue;
         }

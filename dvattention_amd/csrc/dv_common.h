@@ -194,9 +194,10 @@ hipError_t launch_rope(int dtype, const RopeParams& p, hipStream_t stream);
 hipError_t launch_kv_append(int dtype, int rope_dtype, const AppendParams& p, hipStream_t stream);
 hipError_t launch_view_meta(const MetaParams& p, hipStream_t stream);
 
-// Multi-query path (S >= 2 tokens per sequence, 16-bit types): K/V read once per
-// block of 16 tokens.  Rows of DecodeParams are (sequence, 16-token block) groups.
-inline bool use_chunk(int dtype, int S) { return S >= 2 && dtype != kF32; }
+// Multi-query path (S >= 2 tokens per sequence; dv_chunk for 16-bit types,
+// dv_chunk32 for fp32): K/V read once per block of 16 tokens.  Rows of
+// DecodeParams are (sequence, 16-token block) groups.
+inline bool use_chunk(int /*dtype*/, int S) { return S >= 2; }
 size_t chunk_workspace_bytes(int W, int S, int Hkv, int device);
 hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& base, long long max_keys_per_group,
                         void* workspace, size_t ws_bytes, hipStream_t stream);
@@ -205,7 +206,8 @@ hipError_t launch_chunk(int dtype, int qmode, int kvmode, const DecodeParams& ba
 // t < cu_seqlens_q[i + 1]) in groups of up to 16, one K/V stream per group.
 constexpr int kVarlenChunkMaxW = 4096;  // sequences of the group-table pass (LDS)
 inline bool use_varlen_chunk(int dtype, int T, int W) {
-    return dtype != kF32 && W >= 1 && W <= kVarlenChunkMaxW && (long long)T >= 2ll * W;
+    (void)dtype;
+    return W >= 1 && W <= kVarlenChunkMaxW && (long long)T >= 2ll * W;
 }
 size_t varlen_chunk_workspace_bytes(int T, int W, int Hkv, int device);
 hipError_t launch_varlen_chunk(int dtype, const DecodeParams& base, long long max_keys_per_group, void* workspace,

@@ -254,10 +254,14 @@ def as_varlen(wl: Workload) -> Workload:
 
 def workload(key, device="cuda", seed=1234) -> Workload:
     """A configuration by key: 1-5, "5v" (configuration 5 through the varlen op),
-    or "2u" (configuration 2 with every sequence at 8192 keys: the north star's
-    "batch 32 x 8k context" taken literally)."""
+    "5f" (configuration 5's shape in fp32: the fp32 multi-query kernel), or "2u"
+    (configuration 2 with every sequence at 8192 keys: the north star's "batch
+    32 x 8k context" taken literally)."""
     if str(key) == "5v":
         return as_varlen(config(5, device=device, seed=seed))
+    if str(key) == "5f":
+        return paged_workload("cfg5f_chunk_fp32_b16_S16_L8208", W=16, Hkv=8, S=16, lengths=[8192 + 16] * 16, R=32,
+                              base=1e4, bs=16, dtype=torch.float32, device=device, seed=seed, causal_chunk=True)
     if str(key) == "2u":
         return paged_workload("cfg2u_paged_bf16_b32_L8k", W=32, Hkv=8, S=1, lengths=[8192] * 32, R=128, base=1e4,
                               bs=16, dtype=torch.bfloat16, device=device, seed=seed)

@@ -180,7 +180,7 @@ def test_paged_vs_oracle(dv, gpu, dtype, case):
     close(out, ref, dtype, f"paged {case}")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_chunk_causal_block(dv, gpu, dtype):
     # config-5 shape in miniature: 16 new tokens, causal inside the chunk, several pieces per segment
     W, Hkv, S, bs, prior = 3, 2, 16, 16, 2000
@@ -191,7 +191,7 @@ def test_chunk_causal_block(dv, gpu, dtype):
     close(out, O.paged_sdpa(0.1, **d), dtype, "chunk")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_chunk_many_row_groups_multi_launch(dv, gpu, dtype):
     # 2100 sequences x 2 tokens: more 16-token row groups than one launch's
     # schedule holds (2048), so the rows are split over two launches that reuse
@@ -201,7 +201,7 @@ def test_chunk_many_row_groups_multi_launch(dv, gpu, dtype):
     close(out, O.paged_sdpa(0.1, **d), dtype, "multi-launch chunk")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_chunk_views_longest_for_different_tokens(dv, gpu, dtype):
     # token 0 sees all of view 0 and little of view 1, token 1 the reverse: the
     # row group's key space is the per-view union summed over views (3000 keys),
@@ -212,7 +212,7 @@ def test_chunk_views_longest_for_different_tokens(dv, gpu, dtype):
     close(out, O.paged_sdpa(0.1, **d), dtype, "views")
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("dtype", DTYPES)
 def test_chunk_page_cache_subranges_and_invalid_pages(dv, gpu, dtype):
     # S >= 2 (chunk kernel) with one-token pages: a 5000-key view spans three
     # sub-ranges of the kernel's 2048-entry page-id cache; out-of-pool table
