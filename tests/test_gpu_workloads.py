@@ -18,8 +18,9 @@ from test_gpu_parity import close
 pytestmark = pytest.mark.gpu
 
 # rows of each configuration and how many the oracle takes per batch ("2u":
-# configuration 2 with every sequence at 8192 keys, the bench's supplementary row)
-ROWS = {2: (32, 8), "2u": (32, 8), 3: (64, 32), 4: (4, 1), 5: (16, 8)}
+# configuration 2 with every sequence at 8192 keys; "5f": configuration 5's
+# shape in fp32 -- the bench's supplementary rows)
+ROWS = {2: (32, 8), "2u": (32, 8), 3: (64, 32), 4: (4, 1), 5: (16, 8), "5f": (16, 8)}
 
 _cache = {}
 
