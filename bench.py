@@ -9,6 +9,9 @@ inputs already resident in HBM.  The headline line (``value``) is configuration
 2 (bf16 paged GQA-16 decode, batch 32, KV length U[1024, 8192], page 16): K
 steps are timed back to back between two synchronisations; ``value`` is the
 achieved algorithmic HBM rate in TB/s and ``ms_per_step`` the time per call.
+Before each timed region the same calls run untimed for ``--prewarm-ms``
+(default 50 ms) besides the W warm-up steps, so that the GPU's clock has left
+its idle state (its governor takes 10-20 ms of load to reach the steady clock).
 Inputs rotate over enough replicas that consecutive calls never find their K/V
 in the 256 MB Infinity Cache (cold HBM reads, as in a real multi-layer decode
 step).  Every configuration is also reported under ``per_config`` (``5v``:
@@ -64,6 +67,29 @@ def replicas_for(wl_bytes: int, max_replicas: int = 4096) -> int:
 # calls of a 10 us call are dominated by the first launch's host latency.
 MIN_TIMED_US = 2000.0
 
+# Before each timed region the GPU runs the measured calls themselves for at
+# least this long (wall clock), besides the --warmup steps: the shader clock
+# idles at ~100 MHz while the host builds inputs and its governor needs 10-20 ms
+# of load to reach the steady clock (1.7 -> 2.3 GHz measured), so a handful of
+# 0.1 ms warm-up calls would time part of the ramp (configuration 5's first 30
+# calls after a pause: 219 us each, then 185).  --prewarm-ms 0: exactly W
+# warm-up steps.
+PREWARM_MS = 50.0
+
+
+def prewarm(call, ms: float) -> None:
+    """Run call(j) for at least `ms` milliseconds of wall time, in batches of 16
+    between synchronisations (so the queue stays short)."""
+    if ms <= 0:
+        return
+    t0 = time.perf_counter()
+    j = 0
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(16):
+            call(j)
+            j += 1
+        torch.cuda.synchronize()
+
 
 def time_config(i, steps: int, warmup: int, device, exact: bool = False) -> dict:
     """Per-call time of configuration i (1-5, "5v", "5f" or "2u").  exact: time exactly
@@ -75,6 +101,7 @@ def time_config(i, steps: int, warmup: int, device, exact: bool = False) -> dict
     wls = [first] + [WL.workload(i, device=device, seed=1234 + r) for r in range(1, R)]
     outs = [w.out_like() for w in wls]
     rqs = [torch.empty(w.meta["rq_shape"], dtype=w.dtype, device=device) if w.op == "fused" else None for w in wls]
+    prewarm(lambda j: WL.run(wls[j % R], outs[j % R], rqs[j % R]), PREWARM_MS)
     for j in range(warmup):
         WL.run(wls[j % R], outs[j % R], rqs[j % R])
     torch.cuda.synchronize()
@@ -174,6 +201,7 @@ def read_ceiling(i: int, steps: int, warmup: int, device) -> dict:
         if rc != 0:
             raise RuntimeError(lib.dvprobe_last_error().decode())
 
+    prewarm(call, PREWARM_MS)
     for j in range(warmup):
         call(j)
     torch.cuda.synchronize()
@@ -211,6 +239,7 @@ def plain_read(device, gib: int = 4, calls: int = 10) -> dict:
             if lib.dvprobe_plain_read(buf.data_ptr(), nbytes, nt, sink.data_ptr(), sink.numel(),
                                       stream.cuda_stream) != 0:
                 raise RuntimeError(lib.dvprobe_last_error().decode())
+        prewarm(lambda j: call(), PREWARM_MS)
         for _ in range(3):
             call()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -318,6 +347,7 @@ def small_crossover(device, min_us: float = 3000.0) -> dict:
                 row["workgroups"] = W * Hkv * row["chunks"]
                 for mode in ("force", "off"):
                     capi.set_option("small_path", capi.SMALL_PATH[mode])
+                    prewarm(call, PREWARM_MS)
                     for j in range(5):
                         call(j)
                     torch.cuda.synchronize()
@@ -350,6 +380,7 @@ def _time_calls(fn, n_inputs: int, steps: int, warmup: int) -> tuple:
     (HIP events; small kernels are bound by the host's launch rate there) and
     (b) the same calls captured in one HIP graph and replayed (the GPU-side cost
     of a call, as in a graph-captured decode step)."""
+    prewarm(lambda j: fn(j % n_inputs), PREWARM_MS)
     for j in range(warmup):
         fn(j % n_inputs)
     torch.cuda.synchronize()
@@ -509,11 +540,15 @@ def cpu_baseline(device, budget_s: float = 10.0) -> dict:
 
 
 def main() -> int:
+    global PREWARM_MS
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--configs", default="1,2,2u,3,4,5,5v,5f")
+    ap.add_argument("--prewarm-ms", type=float, default=PREWARM_MS,
+                    help="wall-clock ms of untimed calls before each timed region, besides --warmup "
+                         "(the GPU clock's ramp from idle; 0: exactly --warmup steps)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-cache-rows", action="store_true", help="skip the K-side append / view metadata rows")
     ap.add_argument("--read-ceiling", action="store_true",
@@ -523,6 +558,7 @@ def main() -> int:
     ap.add_argument("--small-crossover", action="store_true",
                     help="only the single-launch vs general path timings of dvattn_fused (one JSON line)")
     args = ap.parse_args()
+    PREWARM_MS = args.prewarm_ms
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (the operator has no multi-GPU path); "
               "run with --gpus 1", file=sys.stderr)
@@ -591,6 +627,7 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "prewarm_ms": args.prewarm_ms,
         "ms_per_step": round(head["us_per_call"] / 1e3, 5),
         "higher_is_better": True,
         "scaling": "weak",
