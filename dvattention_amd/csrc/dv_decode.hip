@@ -569,6 +569,10 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
             v.lp0 = 0;
             u32x4 qB[4];
             bool have_q = false;
+            // query loads issued before the page ids' (their round trips overlap)
+            const bool qsplit = q_split<QM>(p);
+            QRaw qr;
+            if (qsplit) fetch_q16<DT, QM, RM>(p, row, f, hkv, qr);
             // sub-ranges whose pages fit the page cache
             const long long span = KVM == kKvPaged ? (long long)(kPc - 1) * p.bs : (1ll << 30);
             for (int sa = l0; sa < l1;) {
@@ -595,7 +599,8 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
                 if (n_st > 1) m1 = issue<KVM>(p, v, pc, ring + kStage, sa + kStep);
                 if (!have_q) {
                     // rotated once per (row, view) while the first stages are in flight
-                    load_q16<DT, QM, RM>(p, row, f, hkv, qB);
+                    if (qsplit) rotate_q16<DT, QM>(qr, qB);
+                    else load_q16<DT, QM, RM>(p, row, f, hkv, qB);
                     // settle the query loads here: a load still pending in qB at the loop
                     // would make the compiler wait for all vector memory in every step
 #pragma unroll

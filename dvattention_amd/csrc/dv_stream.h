@@ -161,6 +161,110 @@ __device__ inline void load_q16(const DecodeParams& p, int row, int f, int hkv, 
     }
 }
 
+// The same operand in two steps, so that its loads can be issued before the
+// piece's page ids are loaded and their round trips overlap: fetch_q16 loads
+// lane (g, n)'s query runs Q[n][c*32 + g*8 + 0..7] (c = 0..3) and, for a
+// rotation over all 128 dims, the cos/sin runs [h*32 + g*8, +8) (h = 0, 1);
+// rotate_q16 then rotates them with load_q16's arithmetic, bit for bit.  With
+// R = 128, dims d and d + 64 pair up, so run c's partner is run c ^ 2 and both
+// use cos/sin run c & 1.  Taken when q_split() holds (pre-rotated queries, or
+// R = 128 with 16-byte aligned cos/sin tables); otherwise load_q16.
+struct QRaw {
+    u32x4 q[4];
+    f32x4 c[2][2], s[2][2];
+};
+
+template <int QM>
+__device__ inline bool q_split(const DecodeParams& p) {
+    return QM == kQPre ||
+           (p.R == kHeadDim && ((reinterpret_cast<uintptr_t>(p.cosv) | reinterpret_cast<uintptr_t>(p.sinv)) & 15) == 0);
+}
+
+template <int DT, int QM, int RM>
+__device__ inline void fetch_q16(const DecodeParams& p, int row, int f, int hkv, QRaw& r) {
+    using raw = typename Tr<DT>::raw;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    const int h = hkv * kGqa + n;
+    const raw* q;
+    const float* cs = nullptr;
+    const float* sn = nullptr;
+    if (QM == kQPre) {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        q = reinterpret_cast<const raw*>(p.q) + ((((long long)f * p.W + w) * p.Hq + h) * p.S + s) * kHeadDim;
+    } else if (QM == kQRotFull) {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        q = reinterpret_cast<const raw*>(p.q) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+        const long long co = (((long long)f * p.W + w) * p.S + s) * p.R;
+        cs = p.cosv + co;
+        sn = p.sinv + co;
+    } else {
+        q = reinterpret_cast<const raw*>(p.q) + ((long long)row * p.Hq + h) * kHeadDim;
+        const long long co = ((long long)f * p.T + row) * (p.R >> 1);
+        cs = p.cosv + co;
+        sn = p.sinv + co;
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) r.q[cc] = ld16(q + cc * 32 + g * 8);
+    if (QM != kQPre) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            r.c[hh][0] = ld16f(cs + hh * 32 + g * 8);
+            r.c[hh][1] = ld16f(cs + hh * 32 + g * 8 + 4);
+            r.s[hh][0] = ld16f(sn + hh * 32 + g * 8);
+            r.s[hh][1] = ld16f(sn + hh * 32 + g * 8 + 4);
+        }
+    }
+}
+
+template <int DT, int QM>
+__device__ inline void rotate_q16(const QRaw& rin, u32x4 (&qB)[4]) {
+#pragma clang fp contract(off)
+    // register tie: the rotation is computed here, after whatever the caller
+    // issued since fetch_q16 (left to itself, the compiler computed it right
+    // after the loads, waiting for them before the page-id loads)
+    QRaw r = rin;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) asm volatile("" : "+v"(r.q[cc]));
+    if (QM != kQPre) {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int k = 0; k < 2; ++k) asm volatile("" : "+v"(r.c[hh][k]), "+v"(r.s[hh][k]));
+    }
+    if (QM == kQPre) {
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) qB[cc] = r.q[cc];
+        return;
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        const bool first = cc < 2;  // dims [0, 64): x c - x' s; [64, 128): x c + x' s
+        const u32x4 x = r.q[cc], xp = r.q[cc ^ 2];
+        uint32_t wd[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t hv[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int k = 2 * t + e;
+                // halves by shifts (a vector element bit-cast to a 16-bit pair
+                // was compiled as a cast of element 0)
+                const float xv = Tr<DT>::tof((uint16_t)(e ? x[t] >> 16 : x[t] & 0xffffu));
+                const float xq = Tr<DT>::tof((uint16_t)(e ? xp[t] >> 16 : xp[t] & 0xffffu));
+                const float c = r.c[cc & 1][k >> 2][k & 3];
+                const float s = r.s[cc & 1][k >> 2][k & 3];
+                const float a = xv * c;
+                const float b = xq * s;
+                const float y = first ? a - b : a + b;
+                hv[e] = Tr<DT>::fromf(y);
+            }
+            wd[t] = hv[0] | (hv[1] << 16);
+        }
+        qB[cc] = u32x4{wd[0], wd[1], wd[2], wd[3]};
+    }
+}
+
 // fp32: lane (g, n) holds Q[n][c*16 + g*4 + 0..3] for c = 0..7.
 template <int QM, int RM>
 __device__ inline void load_q32(const DecodeParams& p, int row, int f, int hkv, f32x4 (&qB)[8]) {
@@ -224,8 +328,10 @@ inline int pick_hpw(int Hkv) {
 }
 
 // Start cost of a piece in the 16-bit decode's work split, in keys: about the
-// time a workgroup needs to restart its pipeline on a new segment.
-constexpr int kPieceCost = 128;
+// time a workgroup needs to restart its pipeline on a new segment (measured
+// against 64, 96, 128 and 160: configurations 2 and 3 ran fastest at 192,
+// configuration 4 within its spread).
+constexpr int kPieceCost = 192;
 
 // Smallest key range worth a workgroup in the decode split.
 constexpr int kDecodeMinKeys = 64;

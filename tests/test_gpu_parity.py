@@ -250,6 +250,34 @@ def test_paged_through_c_abi_matches_torch_op(dv, gpu):
     close(b, O.paged_sdpa(0.1, **d), torch.bfloat16)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_paged_query_load_paths_bit_identical(dv, gpu, dtype):
+    """With R = 128 and 16-byte aligned cos/sin tables the decode kernel issues
+    the query loads before the page ids' and rotates them later; cos/sin at a
+    4-byte offset (allowed by the C ABI) take the one-step query load.  Both
+    rotate with the same arithmetic: outputs equal bit for bit, and match the
+    oracle."""
+    from dvattention_amd import capi
+    d = rand_paged(1, 6, 1, 8, 16, [900], 128, dtype, seed=21)
+    g = to(d, gpu)
+    a = torch.empty(6, 128, 1, 128, dtype=dtype, device=gpu)
+    capi.paged_sdpa(a, 0.08, g["locations"], g["queries"], g["cosines"], g["sines"], g["fragment_lengths"],
+                    g["k_cache"], g["v_cache"], g["block_tables"])
+    shifted = []
+    for t in (g["cosines"], g["sines"]):
+        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=gpu)
+        u = buf[1:].view(t.shape)
+        u.copy_(t)
+        assert u.data_ptr() % 16 == 4
+        shifted.append(u)
+    b = torch.empty_like(a)
+    capi.paged_sdpa(b, 0.08, g["locations"], g["queries"], shifted[0], shifted[1], g["fragment_lengths"],
+                    g["k_cache"], g["v_cache"], g["block_tables"])
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    close(a, O.paged_sdpa(0.08, **d), dtype)
+
+
 def test_paged_page_permutation_bit_exact(dv, gpu):
     d = rand_paged(2, 3, 1, 8, 16, [257, 130], 128, torch.bfloat16, seed=8, extra_pages=0)
     a = run_paged(dv, d, 0.09, gpu)
