@@ -676,8 +676,8 @@ __global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
     const int HPW = p.hpw;
     long long* s_pref = reinterpret_cast<long long*>(smem + HPW * stream::kWaveLds);
     unsigned char* wlds = smem + wv * stream::kWaveLds;
-    run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<KVM, RM>(p, row); },
-                 [&](int row, int hg, long long v0, long long v1, bool fin, int slot, long long rk) {
+    run_schedule<true>(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<KVM, RM>(p, row); },
+                       [&](int row, int hg, long long v0, long long v1, bool fin, int slot, long long rk) {
         if (wv < HPW) stream::piece<DT, QM, KVM, RM, MV>(p, wlds, row, hg * HPW + wv, v0, v1, fin, slot, wv, rk);
     });
 }

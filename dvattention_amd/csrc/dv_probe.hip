@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void dv_read_probe(const DecodeParams p, unsig
     long long* s_pref = reinterpret_cast<long long*>(smem + HPW * stream::kWaveLds);
     unsigned char* wlds = smem + wv * stream::kWaveLds;
     unsigned acc = 0;
-    run_schedule(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<kKvPaged, kRowWS>(p, row); },
+    run_schedule<true>(p, p.Hkv / HPW, s_pref, s_scan, [&](int row) { return row_visible<kKvPaged, kRowWS>(p, row); },
                  [&](int row, int hg, long long v0, long long v1, bool, int, long long rk) {
         if (wv < HPW) acc += read_piece(p, wlds, row, hg * HPW + wv, v0, v1, rk);
     });
