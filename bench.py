@@ -259,7 +259,8 @@ def plain_read(device, gib: int = 4, calls: int = 10) -> dict:
 def mfma_ceiling(device, iters: int = 2000, calls: int = 10) -> dict:
     """The MFMA rate probe (dv_probe.hip `dvprobe_mfma_rate`): back-to-back
     v_mfma_f32_16x16x32_bf16 on every SIMD at the chunk kernel's occupancy (eight
-    waves per CU), alone and with n independent fp32 FMAs or v_exp_f32 per MFMA.
+    waves per CU), alone and with n independent fp32 FMAs or v_exp_f32 per MFMA;
+    then v_mfma_f32_32x32x16_bf16 with n FMAs per MFMA (`dvprobe_mfma_rate32`).
     Per mix: TFLOP/s, the shader clock the waves ran at (s_memtime against the
     100 MHz s_memrealtime counter), and SIMD cycles per MFMA at that clock."""
     import ctypes
@@ -293,8 +294,37 @@ def mfma_ceiling(device, iters: int = 2000, calls: int = 10) -> dict:
         ck = clocks.view(-1, 2).double().sum(0).tolist()
         mhz = ck[0] / ck[1] * 100.0 if ck[1] > 0 else 0.0
         mfma_per_simd = iters * 8 * 2                 # two waves per SIMD, eight MFMAs per round
-        rows.append({"other_per_mfma": n, "kind": "exp" if ex else "fma", "us": round(us, 1),
+        rows.append({"shape": "16x16x32", "other_per_mfma": n, "kind": "exp" if ex else "fma", "us": round(us, 1),
                      "tflops": round(wgs * 8 * iters * 8 * 16384 / (us * 1e-6) / 1e12, 1),
+                     "clock_mhz": round(mhz), "simd_cycles_per_mfma": round(mhz * us / mfma_per_simd, 2)})
+    # v_mfma_f32_32x32x16_bf16 (twice the work per instruction, half the rounds):
+    # n FMAs per MFMA = n/2 per 16x16x32-equivalent
+    lib.dvprobe_mfma_rate32.restype = ctypes.c_int
+    lib.dvprobe_mfma_rate32.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_longlong,
+                                        ctypes.c_void_p, ctypes.c_longlong, ctypes.c_void_p]
+    it32 = iters // 2
+    for n in (0, 2, 4, 6, 8, 12):
+        def call():
+            wgs = lib.dvprobe_mfma_rate32(n, it32, sink.data_ptr(), sink.numel(), clocks.data_ptr(),
+                                          clocks.numel(), stream.cuda_stream)
+            if wgs < 0:
+                raise RuntimeError(lib.dvprobe_last_error().decode())
+            return wgs
+        for _ in range(2):
+            wgs = call()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        for _ in range(calls):
+            call()
+        b.record(stream)
+        torch.cuda.synchronize()
+        us = a.elapsed_time(b) * 1e3 / calls
+        ck = clocks.view(-1, 2).double().sum(0).tolist()
+        mhz = ck[0] / ck[1] * 100.0 if ck[1] > 0 else 0.0
+        mfma_per_simd = it32 * 8 * 2
+        rows.append({"shape": "32x32x16", "other_per_mfma": n, "kind": "fma", "us": round(us, 1),
+                     "tflops": round(wgs * 8 * it32 * 8 * 32768 / (us * 1e-6) / 1e12, 1),
                      "clock_mhz": round(mhz), "simd_cycles_per_mfma": round(mhz * us / mfma_per_simd, 2)})
     return {"cus": cus, "iters": iters, "rows": rows}
 
@@ -588,7 +618,7 @@ def main() -> int:
     if args.mfma_ceiling:
         res = mfma_ceiling(device)
         for r in res["rows"]:
-            log(f"[bench] mfma 16x16x32 bf16 + {r['other_per_mfma']} {r['kind']}/MFMA: {r['tflops']} TFLOP/s at "
+            log(f"[bench] mfma {r['shape']} bf16 + {r['other_per_mfma']} {r['kind']}/MFMA: {r['tflops']} TFLOP/s at "
                 f"{r['clock_mhz']} MHz, {r['simd_cycles_per_mfma']} SIMD cycles per MFMA")
         print(json.dumps({"mfma_ceiling": res}), flush=True)
         return 0

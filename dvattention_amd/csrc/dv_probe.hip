@@ -158,6 +158,50 @@ __global__ __launch_bounds__(512) void dv_mfma_rate(float* sink, unsigned long l
     }
 }
 
+// The same with v_mfma_f32_32x32x16_bf16 (twice the work per instruction,
+// sixteen accumulators per lane): N other instructions per MFMA here equal N/2
+// per 16x16x32-equivalent of matrix work.
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+
+template <int N>
+__global__ __launch_bounds__(512) void dv_mfma_rate32(float* sink, unsigned long long* clocks, int iters) {
+    constexpr int kChains = 8;
+    constexpr int kX = N > 0 ? N : 1;
+    const int lane = threadIdx.x & 63;
+    const u32x4 a = {0x3f803f80u ^ (unsigned)lane, 0x3f003f00u, 0x3e803e80u + (unsigned)lane, 0x3f803f00u};
+    const u32x4 b = {0x3f003f80u, 0x3e803f80u ^ (unsigned)(lane << 3), 0x3f803f80u, 0x3f003f00u};
+    f32x16 c[kChains];
+#pragma unroll
+    for (int i = 0; i < kChains; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) c[i][e] = 0.f;
+    float x[kX];
+#pragma unroll
+    for (int v = 0; v < kX; ++v) x[v] = (float)(lane + v) * 0.01f;
+    const unsigned long long t0 = __builtin_amdgcn_s_memtime(), r0 = __builtin_amdgcn_s_memrealtime();
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int i = 0; i < kChains; ++i) {
+            c[i] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b),
+                                                           c[i], 0, 0, 0);
+#pragma unroll
+            for (int v = 0; v < N; ++v) x[v] = __builtin_fmaf(x[v], 0.999f, 0.5f);
+        }
+    }
+    const unsigned long long t1 = __builtin_amdgcn_s_memtime(), r1 = __builtin_amdgcn_s_memrealtime();
+    float s = 0.f;
+#pragma unroll
+    for (int v = 0; v < kX; ++v) s += x[v];
+#pragma unroll
+    for (int i = 0; i < kChains; ++i) s += c[i][0] + c[i][5] + c[i][10] + c[i][15];
+    sink[(size_t)blockIdx.x * blockDim.x + threadIdx.x] = s;
+    const int w = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+    if (lane == 0) {
+        clocks[2 * w] = t1 - t0;
+        clocks[2 * w + 1] = r1 - r0;
+    }
+}
+
 thread_local const char* g_msg = "";
 
 }  // namespace
@@ -320,6 +364,45 @@ __attribute__((visibility("default"))) int dvprobe_mfma_rate(int n_other, int ex
     }
     if (!k) {
         g_msg = "probe: unsupported mix (FMAs: 0, 1, 2, 3, 4, 6; exponentials: 1, 2)";
+        return -1;
+    }
+    hipLaunchKernelGGL(k, dim3(cus), dim3(512), 0, (hipStream_t)stream, sink, clocks, iters);
+    if (hipGetLastError() != hipSuccess) {
+        g_msg = "probe: launch failed";
+        return -1;
+    }
+    g_msg = "";
+    return cus;
+}
+
+// dvprobe_mfma_rate with v_mfma_f32_32x32x16_bf16 and n_other fp32 FMAs per MFMA
+// (0, 2, 4, 6, 8, 12).  Same arguments and return value.
+__attribute__((visibility("default"))) int dvprobe_mfma_rate32(int n_other, int iters, float* sink,
+                                                                long long sink_floats, unsigned long long* clocks,
+                                                                long long clock_words, void* stream) {
+    using namespace dv;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess) {
+        g_msg = "probe: no device";
+        return -1;
+    }
+    const int cus = device_cu_count(device);
+    if (!sink || !clocks || iters <= 0 || sink_floats < 512ll * cus || clock_words < 16ll * cus) {
+        g_msg = "probe: mfma rate needs iters > 0, 512 sink floats and 16 clock words per CU";
+        return -1;
+    }
+    void (*k)(float*, unsigned long long*, int) = nullptr;
+    switch (n_other) {
+        case 0: k = dv_mfma_rate32<0>; break;
+        case 2: k = dv_mfma_rate32<2>; break;
+        case 4: k = dv_mfma_rate32<4>; break;
+        case 6: k = dv_mfma_rate32<6>; break;
+        case 8: k = dv_mfma_rate32<8>; break;
+        case 12: k = dv_mfma_rate32<12>; break;
+        default: break;
+    }
+    if (!k) {
+        g_msg = "probe: unsupported mix (FMAs: 0, 2, 4, 6, 8, 12)";
         return -1;
     }
     hipLaunchKernelGGL(k, dim3(cus), dim3(512), 0, (hipStream_t)stream, sink, clocks, iters);
