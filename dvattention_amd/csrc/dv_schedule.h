@@ -87,8 +87,9 @@ __device__ inline void split_chunks(const DecodeParams& p, int NHG, long long to
     const int gidx = blockIdx.x;
     if (gidx >= geff) return;
 
-    long long u = bound(gidx);
+    const long long u0 = bound(gidx);
     const long long uend = bound(gidx + 1);
+    long long u = u0;
     int r = find_row(u);
     while (u < uend && r < nrows) {
         const long long pr = pref_u(r);
@@ -105,9 +106,12 @@ __device__ inline void split_chunks(const DecodeParams& p, int NHG, long long to
         const long long b = uend < segc + D ? uend : segc + D;
         if (a < b) {
             const int sg = r * NHG + hg;
-            const long long gf = chunk_of(ka), gl = chunk_of(segc + D - 1);
-            const int slot = sg + gidx;  // = first slot of the segment (gf + sg) + piece index (gidx - gf)
-            piece(p.row_begin + r, hg, a - ka, b - ka, gl == gf, slot, D - c);
+            // the segment has no other piece iff its first and last keys both lie
+            // in this chunk (chunk_of(ka) == chunk_of(segc + D - 1) == gidx, without
+            // the divisions)
+            const bool fin = ka >= u0 && segc + D - 1 < uend;
+            const int slot = sg + gidx;  // = first slot of the segment (chunk_of(ka) + sg) + piece index
+            piece(p.row_begin + r, hg, a - ka, b - ka, fin, slot, D - c);
         }
         u = segc + D;
     }
