@@ -134,18 +134,35 @@ __device__ inline int loc_of(const DecodeParams& p, int f, const Grp& g, int i) 
 // walks (view f's keys follow the longest range of views 0 .. f-1).  The max
 // over tokens of the per-token sum is shorter whenever different tokens see
 // most in different views, and would leave the tail of the key space unassigned.
+// View f's visible count, the largest over the tokens of group g: the tokens'
+// locations are loaded together (one round trip instead of one per token; the
+// loads are unconditional, on a clamped token index, so none waits behind a
+// branch); a token past the group's end counts as location -1, which sees no
+// key.  (A group without tokens -- varlen padding, first token 0 -- reads token
+// 0's location and discards it.)
+template <int KVM, int RM>
+__device__ inline int group_view_vis(const DecodeParams& p, int f, const Grp& g) {
+    const int last = g.ntok > 0 ? g.ntok - 1 : 0;
+    int lc[kTokBlk];
+#pragma unroll
+    for (int i = 0; i < kTokBlk; ++i) {
+        const int x = loc_of<RM>(p, f, g, i < last ? i : last);
+        lc[i] = i < g.ntok ? x : -1;
+    }
+    int best = 0;
+#pragma unroll
+    for (int i = 0; i < kTokBlk; ++i) {
+        const int v = view_vis<KVM>(p, f, lc[i]);
+        best = v > best ? v : best;
+    }
+    return best;
+}
+
 template <int KVM, int RM>
 __device__ inline long long group_visible(const DecodeParams& p, int rg) {
     const Grp g = group_of<RM>(p, rg);
     long long total = 0;
-    for (int f = 0; f < p.F; ++f) {
-        int best = 0;
-        for (int i = 0; i < g.ntok; ++i) {
-            const int v = view_vis<KVM>(p, f, loc_of<RM>(p, f, g, i));
-            best = v > best ? v : best;
-        }
-        total += best;
-    }
+    for (int f = 0; f < p.F; ++f) total += group_view_vis<KVM, RM>(p, f, g);
     return total;
 }
 

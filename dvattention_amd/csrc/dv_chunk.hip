@@ -465,12 +465,8 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
     long long P = 0, off = 0;
     for (int f = 0; f < p.F && P < v1; ++f) {
         // visible keys of this view for the block (union) and per tile
-        int vis_blk = 0;
+        const int vis_blk = group_view_vis<KVM, RM>(p, f, gr);
         int vis_t[kTiles];
-        for (int i = 0; i < gr.ntok; ++i) {
-            const int v = view_vis<KVM>(p, f, loc_of<RM>(p, f, gr, i));
-            vis_blk = v > vis_blk ? v : vis_blk;
-        }
 #pragma unroll
         for (int t = 0; t < kTiles; ++t)  // wave-uniform: the stage masks and their branches stay scalar
             vis_t[t] = __builtin_amdgcn_readfirstlane(t < ntile ? view_vis<KVM>(p, f, loc_of<RM>(p, f, gr, tok0 + t)) : 0);

@@ -215,11 +215,7 @@ __device__ void chunk32_piece(const DecodeParams& p, unsigned char* smem, int* p
 
     long long P = 0, off = 0;
     for (int f = 0; f < p.F && P < v1; ++f) {
-        int vis_blk = 0;
-        for (int i = 0; i < gr.ntok; ++i) {
-            const int v = view_vis<KVM>(p, f, loc_of<RM>(p, f, gr, i));
-            vis_blk = v > vis_blk ? v : vis_blk;
-        }
+        const int vis_blk = group_view_vis<KVM, RM>(p, f, gr);
         int vis_t[kT32];
 #pragma unroll
         for (int t = 0; t < kT32; ++t)
