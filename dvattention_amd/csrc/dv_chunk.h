@@ -166,6 +166,36 @@ __device__ inline long long group_visible(const DecodeParams& p, int rg) {
     return total;
 }
 
+// Page-cache fill of a chunk workgroup (kThreads threads): pages[i] = entry
+// lp0 + i of the sequence's block_tables row bt, for i < kPageCap (-1 past the
+// row or outside [0, num_blocks)).  Each thread issues all of its loads (on
+// clamped, in-bounds indices) before the first is waited for, where a strided
+// loop waited once per pass.  Returns whether this thread's entries up to
+// logical page lpl are all valid.
+__device__ inline bool fill_page_cache(const DecodeParams& p, const int* bt, int* pages, uint32_t lp0, uint32_t lpl) {
+    constexpr int kIt = kPageCap / kThreads;
+    static_assert(kIt * kThreads == kPageCap, "page cache entries per thread");
+    const int tid = threadIdx.x;
+    const uint32_t maxB = (uint32_t)p.maxB;
+    int pg[kIt];
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+        const uint32_t lp = lp0 + (uint32_t)(tid + k * kThreads);
+        pg[k] = -1;
+        if (maxB > 0) pg[k] = bt[lp < maxB ? lp : maxB - 1];
+    }
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+        const uint32_t lp = lp0 + (uint32_t)(tid + k * kThreads);
+        int v = lp < maxB ? pg[k] : -1;
+        if (v < 0 || v >= p.nblocks) v = -1;
+        pages[tid + k * kThreads] = v;
+        if (lp <= lpl && v < 0) ok = false;
+    }
+    return ok;
+}
+
 __device__ inline uint32_t token_mask(int vis, int kb0) {
     const int lim = vis - kb0;
     return lim >= 32 ? 0xffffffffu : (lim <= 0 ? 0u : ((1u << lim) - 1u));

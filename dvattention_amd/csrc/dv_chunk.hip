@@ -509,17 +509,8 @@ __device__ void chunk_piece(const DecodeParams& p, unsigned char* smem, int* pag
                     const uint32_t lpl = p.bs_shift >= 0 ? (p1 >> p.bs_shift) : p1 / (uint32_t)p.bs;
                     r.lp0 = p.bs_shift >= 0 ? (p0 >> p.bs_shift) : p0 / (uint32_t)p.bs;
                     __syncthreads();
-                    bool ok = true;  // every page this thread loaded for the sub-range is valid
-                    for (int i = tid; i < kPageCap; i += blockDim.x) {
-                        const uint32_t lp = r.lp0 + (uint32_t)i;
-                        int pg = -1;
-                        if (lp < (uint32_t)p.maxB) {
-                            pg = p.bt[(long long)w * p.maxB + lp];
-                            if (pg < 0 || pg >= p.nblocks) pg = -1;
-                        }
-                        pages[i] = pg;
-                        if (lp <= lpl && pg < 0) ok = false;
-                    }
+                    // every page this thread loaded for the sub-range is valid
+                    const bool ok = fill_page_cache(p, p.bt + (long long)w * p.maxB, pages, r.lp0, lpl);
                     r.pages_ok = __syncthreads_and(ok) != 0;
                 }
                 stream_range<DT, KVM, P2>(p, r, pages, smem, sa, sbnd, vis_t, qB, tl);

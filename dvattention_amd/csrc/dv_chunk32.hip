@@ -262,15 +262,8 @@ __device__ void chunk32_piece(const DecodeParams& p, unsigned char* smem, int* p
                     const uint32_t p0 = (uint32_t)(off + sa);
                     r.lp0 = p.bs_shift >= 0 ? (p0 >> p.bs_shift) : p0 / (uint32_t)p.bs;
                     __syncthreads();  // every wave is done with the previous sub-range's page ids
-                    for (int i = tid; i < kPageCap; i += blockDim.x) {
-                        const uint32_t lp = r.lp0 + (uint32_t)i;
-                        int pg = -1;
-                        if (lp < (uint32_t)p.maxB) {
-                            pg = p.bt[(long long)w * p.maxB + lp];
-                            if (pg < 0 || pg >= p.nblocks) pg = -1;
-                        }
-                        pages[i] = pg;
-                    }
+                    static_assert(kWaves32 * kWave == kThreads, "one page-cache fill per workgroup");
+                    fill_page_cache(p, p.bt + (long long)w * p.maxB, pages, r.lp0, 0u);
                     __syncthreads();
                 }
                 stream32<KVM, P2>(p, r, pages, smem, sa, sbnd, nt, vis_t, qB, tl);

@@ -413,17 +413,15 @@ __device__ bool views_stream(const DecodeParams& p, unsigned char* wlds, int row
     }
     pcb[kStreamViews] = npages;
     if (npages > kPc) return false;
-    const int* bt = p.bt + (long long)w * p.maxB;
+    // the views' page ids in one fill: entry i belongs to the last view j with
+    // pcb[j] <= i (selects with constant indices, no dynamically indexed array)
+    fill_pages(p, p.bt + (long long)w * p.maxB, pc, npages, [&](int i) {
+        uint32_t lp = (uint32_t)lpa[0] + (uint32_t)i;
 #pragma unroll
-    for (int j = 0; j < kStreamViews; ++j) {
-        const int need = pcb[j + 1] - pcb[j];
-        for (int i = lane; i < need; i += kWave) {
-            const uint32_t lp = (uint32_t)lpa[j] + (uint32_t)i;
-            int pg = lp < (uint32_t)p.maxB ? bt[lp] : -1;
-            if (pg < 0 || pg >= p.nblocks) pg = -1;
-            pc[pcb[j] + i] = pg;
-        }
-    }
+        for (int j = 1; j < kStreamViews; ++j)
+            if (i >= pcb[j]) lp = (uint32_t)lpa[j] + (uint32_t)(i - pcb[j]);
+        return lp;
+    });
 
     // issue cursor: view ji, next key li; the view's parameters are copied out of
     // the per-view arrays with constant indices (no dynamically indexed arrays,
@@ -585,13 +583,8 @@ __device__ void piece(const DecodeParams& p, unsigned char* wlds, int row, int h
                     page_split(p, pz > 0 ? (uint32_t)pz : 0u, lpz, r);
                     v.lp0 = (int)lpa;
                     const int need = (int)(lpz - lpa) + 1;
-                    const int* bt = p.bt + (long long)w * p.maxB;
-                    for (int i = lane; i < need; i += kWave) {
-                        const uint32_t lp = lpa + (uint32_t)i;
-                        int pg = lp < (uint32_t)p.maxB ? bt[lp] : -1;
-                        if (pg < 0 || pg >= p.nblocks) pg = -1;
-                        pc[i] = pg;
-                    }
+                    fill_pages(p, p.bt + (long long)w * p.maxB, pc, need,
+                               [&](int i) { return lpa + (uint32_t)i; });
                 }
                 const int n_st = (sb - sa + kStep - 1) / kStep;
                 uint32_t m0 = issue<KVM>(p, v, pc, ring, sa);

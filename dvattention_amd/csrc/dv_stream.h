@@ -353,6 +353,40 @@ constexpr int kRing = 2;                     // stages per wave
 constexpr int kPc = 512;                     // page ids cached per wave
 constexpr int kWaveLds = kRing * kStage + kPc * 4;
 
+// Page-cache fill of one wave: pc[i] = block_tables row entry lp_of(i) for i in
+// [0, n) (n <= kPc), -1 for an entry past the row or a page id outside
+// [0, num_blocks).  All of the wave's loads are issued before the first is
+// waited for (a loop that stored each pass's ids before loading the next paid
+// one memory round trip per 64 entries): every pass loads from a clamped,
+// in-bounds index, and the range checks and LDS stores follow in a second pass.
+template <class LpOf>
+__device__ inline void fill_pages(const DecodeParams& p, const int* bt, int* pc, int n, LpOf&& lp_of) {
+    constexpr int kIt = kPc / kWave;
+    const int lane = threadIdx.x & 63;
+    const uint32_t maxB = (uint32_t)p.maxB;
+    const int nk = (n + kWave - 1) / kWave;  // passes with entries (wave-uniform)
+    if (n <= 0) return;
+    int pg[kIt];
+    uint32_t ok = 0;  // bit k: entry lane + 64k exists and lies in the row
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+        const int i = lane + k * kWave;
+        const uint32_t lp = lp_of(i < n ? i : n - 1);
+        ok |= (i < n && lp < maxB) ? (1u << k) : 0u;
+        pg[k] = -1;
+        if (k < nk && maxB > 0) pg[k] = bt[lp < maxB ? lp : maxB - 1];
+    }
+#pragma unroll
+    for (int k = 0; k < kIt; ++k) {
+        const int i = lane + k * kWave;
+        if (k < nk && i < n) {
+            int v = ((ok >> k) & 1u) ? pg[k] : -1;
+            if (v < 0 || v >= p.nblocks) v = -1;
+            pc[i] = v;
+        }
+    }
+}
+
 struct View {
     const unsigned char* k;  // paged: the cache; contiguous: K row 0 of (batch entry, head)
     const unsigned char* v;
