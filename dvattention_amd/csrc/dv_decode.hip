@@ -413,6 +413,19 @@ __device__ bool views_stream(const DecodeParams& p, unsigned char* wlds, int row
     }
     pcb[kStreamViews] = npages;
     if (npages > kPc) return false;
+    // query loads issued before the page ids' (their round trips overlap): the
+    // row's query runs once and every view's cos/sin run (R of 32 or 64),
+    // rotated per view once the first stages are issued, so the first compute
+    // waits for stage 0 alone
+    const bool qsplit = q_split_narrow<QM>(p);
+    u32x4 qrow[4];
+    QCs1 vcs[kStreamViews];
+    if (qsplit) {
+        fetch_qrow16<DT, QM, RM>(p, row, hkv, qrow);
+#pragma unroll
+        for (int j = 0; j < kStreamViews; ++j)
+            if (ns[j] > 0) fetch_cs16_narrow<QM>(p, row, vf[j], vcs[j]);
+    }
     // the views' page ids in one fill: entry i belongs to the last view j with
     // pcb[j] <= i (selects with constant indices, no dynamically indexed array)
     fill_pages(p, p.bt + (long long)w * p.maxB, pc, npages, [&](int i) {
@@ -464,7 +477,8 @@ __device__ bool views_stream(const DecodeParams& p, unsigned char* wlds, int row
 #pragma unroll
     for (int j = 0; j < kStreamViews; ++j) {
         if (ns[j] > 0) {
-            load_q16<DT, QM, RM>(p, row, vf[j], hkv, q[j]);
+            if (qsplit) rotate_q16_narrow<DT>(p, qrow, vcs[j], q[j]);
+            else load_q16<DT, QM, RM>(p, row, vf[j], hkv, q[j]);
         } else {
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) q[j][cc] = u32x4{0u, 0u, 0u, 0u};

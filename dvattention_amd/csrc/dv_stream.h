@@ -265,6 +265,116 @@ __device__ inline void rotate_q16(const QRaw& rin, u32x4 (&qB)[4]) {
     }
 }
 
+// Multi-view pieces with a rotary width R of 32 or 64: the row's query runs
+// are loaded once (fetch_qrow16, same lanes and runs as fetch_q16) and each
+// view's cos/sin run separately (fetch_cs16_narrow: one 8-dim run per lane, at
+// (g·8) mod R/2), all before the page ids; rotate_q16_narrow then gives
+// load_q16's operand bit for bit.  Dim d pairs with d ± R/2: for R = 64 run c's
+// partner is run c ^ 1 (same lane), for R = 32 run 0 of lane ^ 32 (g ^ 2);
+// runs from c·32 >= R pass through.  Taken when q_split_narrow() holds.
+struct QCs1 {
+    f32x4 c[2], s[2];
+};
+
+template <int QM>
+__device__ inline bool q_split_narrow(const DecodeParams& p) {
+    return QM != kQPre && (p.R == 32 || p.R == 64) &&
+           ((reinterpret_cast<uintptr_t>(p.cosv) | reinterpret_cast<uintptr_t>(p.sinv)) & 15) == 0;
+}
+
+template <int DT, int QM, int RM>
+__device__ inline void fetch_qrow16(const DecodeParams& p, int row, int hkv, u32x4 (&q4)[4]) {
+    using raw = typename Tr<DT>::raw;
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, n = lane & 15;
+    const int h = hkv * kGqa + n;
+    const raw* q;
+    if (QM == kQRotFull) {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        q = reinterpret_cast<const raw*>(p.q) + (((long long)w * p.Hq + h) * p.S + s) * kHeadDim;
+    } else {
+        q = reinterpret_cast<const raw*>(p.q) + ((long long)row * p.Hq + h) * kHeadDim;
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) q4[cc] = ld16(q + cc * 32 + g * 8);
+}
+
+template <int QM>
+__device__ inline void fetch_cs16_narrow(const DecodeParams& p, int row, int f, QCs1& r) {
+    const int g = (threadIdx.x & 63) >> 4;
+    const int half = p.R >> 1;
+    long long co;
+    if (QM == kQRotFull) {
+        const int w = row / p.S, s = row - (row / p.S) * p.S;
+        co = (((long long)f * p.W + w) * p.S + s) * p.R;
+    } else {
+        co = ((long long)f * p.T + row) * half;
+    }
+    const int ci = (g * 8) & (half - 1);
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        r.c[hh] = ld16f(p.cosv + co + ci + 4 * hh);
+        r.s[hh] = ld16f(p.sinv + co + ci + 4 * hh);
+    }
+}
+
+template <int DT>
+__device__ inline void rotate_q16_narrow(const DecodeParams& p, const u32x4 (&qin)[4], const QCs1& csin,
+                                         u32x4 (&qB)[4]) {
+#pragma clang fp contract(off)
+    // register tie: rotated here, after whatever the caller issued since the
+    // fetch (else the compiler computes it right after the loads, waiting for
+    // them before the page-id loads)
+    u32x4 q[4];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        q[cc] = qin[cc];
+        asm volatile("" : "+v"(q[cc]));
+    }
+    QCs1 cs = csin;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) asm volatile("" : "+v"(cs.c[k]), "+v"(cs.s[k]));
+    const int g = (threadIdx.x & 63) >> 4;
+    const bool r64 = p.R == 64;
+    u32x4 x32 = q[0];
+    if (!r64) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x32[e] = (uint32_t)__shfl_xor((int)q[0][e], 32, kWave);
+    }
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+        if (cc >= 2 || (cc == 1 && !r64)) {  // dims past the rotary width pass through
+            qB[cc] = q[cc];
+            continue;
+        }
+        // first half: x c - x' s; second: x c + x' s
+        const bool first = r64 ? cc == 0 : g < 2;
+        const u32x4 x = q[cc];
+        const u32x4 xp = r64 ? q[cc ^ 1] : x32;
+        uint32_t wd[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            uint32_t hv[2];
+#pragma unroll
+            for (int e = 0; e < 2; ++e) {
+                const int k = 2 * t + e;
+                // halves by shifts (a vector element bit-cast to a 16-bit pair
+                // was compiled as a cast of element 0)
+                const float xv = Tr<DT>::tof((uint16_t)(e ? x[t] >> 16 : x[t] & 0xffffu));
+                const float xq = Tr<DT>::tof((uint16_t)(e ? xp[t] >> 16 : xp[t] & 0xffffu));
+                const float c = cs.c[k >> 2][k & 3];
+                const float s = cs.s[k >> 2][k & 3];
+                const float a = xv * c;
+                const float b = xq * s;
+                const float y = first ? a - b : a + b;
+                hv[e] = Tr<DT>::fromf(y);
+            }
+            wd[t] = hv[0] | (hv[1] << 16);
+        }
+        qB[cc] = u32x4{wd[0], wd[1], wd[2], wd[3]};
+    }
+}
+
 // fp32: lane (g, n) holds Q[n][c*16 + g*4 + 0..3] for c = 0..7.
 template <int QM, int RM>
 __device__ inline void load_q32(const DecodeParams& p, int row, int f, int hkv, f32x4 (&qB)[8]) {

@@ -250,29 +250,36 @@ def test_paged_through_c_abi_matches_torch_op(dv, gpu):
     close(b, O.paged_sdpa(0.1, **d), torch.bfloat16)
 
 
+def _shifted(t, gpu):
+    """A copy of t whose data starts 4 bytes past a 16-byte boundary."""
+    buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=gpu)
+    u = buf[1:].view(t.shape)
+    u.copy_(t)
+    assert u.data_ptr() % 16 == 4
+    return u
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-def test_paged_query_load_paths_bit_identical(dv, gpu, dtype):
-    """With R = 128 and 16-byte aligned cos/sin tables the decode kernel issues
-    the query loads before the page ids' and rotates them later; cos/sin at a
+@pytest.mark.parametrize("R", [32, 64, 128])
+@pytest.mark.parametrize("F", [1, 3])
+def test_paged_query_load_paths_bit_identical(dv, gpu, dtype, R, F):
+    """With R in {32, 64, 128} and 16-byte aligned cos/sin tables the decode
+    kernel issues the query loads before the page ids' and rotates them later
+    (one view: query and cos/sin runs; several views streamed in one piece: the
+    row's query runs once and each view's cos/sin, R <= 64); cos/sin at a
     4-byte offset (allowed by the C ABI) take the one-step query load.  Both
     rotate with the same arithmetic: outputs equal bit for bit, and match the
     oracle."""
     from dvattention_amd import capi
-    d = rand_paged(1, 6, 1, 8, 16, [900], 128, dtype, seed=21)
+    lens = [900] if F == 1 else [300, 260, 410]
+    d = rand_paged(F, 6, 1, 8, 16, lens, R, dtype, seed=21 + R + F)
     g = to(d, gpu)
     a = torch.empty(6, 128, 1, 128, dtype=dtype, device=gpu)
     capi.paged_sdpa(a, 0.08, g["locations"], g["queries"], g["cosines"], g["sines"], g["fragment_lengths"],
                     g["k_cache"], g["v_cache"], g["block_tables"])
-    shifted = []
-    for t in (g["cosines"], g["sines"]):
-        buf = torch.empty(t.numel() + 1, dtype=t.dtype, device=gpu)
-        u = buf[1:].view(t.shape)
-        u.copy_(t)
-        assert u.data_ptr() % 16 == 4
-        shifted.append(u)
     b = torch.empty_like(a)
-    capi.paged_sdpa(b, 0.08, g["locations"], g["queries"], shifted[0], shifted[1], g["fragment_lengths"],
-                    g["k_cache"], g["v_cache"], g["block_tables"])
+    capi.paged_sdpa(b, 0.08, g["locations"], g["queries"], _shifted(g["cosines"], gpu), _shifted(g["sines"], gpu),
+                    g["fragment_lengths"], g["k_cache"], g["v_cache"], g["block_tables"])
     torch.cuda.synchronize()
     assert torch.equal(a, b)
     close(a, O.paged_sdpa(0.08, **d), dtype)
@@ -429,6 +436,29 @@ def test_varlen_vs_oracle(dv, gpu, dtype, case):
     out = run_varlen(dv, d, 0.088, gpu)
     ref = O.varlen_paged_sdpa(0.088, **d)
     close(out, ref, dtype, f"varlen {case}")
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("R", [32, 64])
+def test_varlen_multiview_query_load_paths_bit_identical(dv, gpu, dtype, R):
+    """Varlen rows over several views (configuration 3's shape of call): the
+    early query load of the multi-view stream (the row's query runs once, each
+    view's half-width cos/sin) against the one-step load forced by cos/sin at a
+    4-byte offset -- equal bit for bit, and equal to the oracle."""
+    from dvattention_amd import capi
+    d = rand_varlen(3, 8, 8, list(range(9)), 4, 16, [400, 350, 500], R, dtype, seed=40 + R)
+    d["locations"] = torch.from_numpy(np.random.default_rng(5).integers(100, 350, size=(3, 8)).astype(np.int32))
+    g = to(d, gpu)
+    a = torch.empty(8, 64, 128, dtype=dtype, device=gpu)
+    capi.varlen_paged_sdpa(a, 0.07, g["locations"], g["queries"], g["cosines"], g["sines"], g["fragment_lengths"],
+                           g["k_cache"], g["v_cache"], g["block_tables"], g["cu_seqlens_q"], g["cu_seqlens_k"])
+    b = torch.empty_like(a)
+    capi.varlen_paged_sdpa(b, 0.07, g["locations"], g["queries"], _shifted(g["cosines"], gpu),
+                           _shifted(g["sines"], gpu), g["fragment_lengths"], g["k_cache"], g["v_cache"],
+                           g["block_tables"], g["cu_seqlens_q"], g["cu_seqlens_k"])
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+    close(a, O.varlen_paged_sdpa(0.07, **d), dtype)
 
 
 def test_varlen_through_c_abi(dv, gpu):
