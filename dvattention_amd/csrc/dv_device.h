@@ -434,32 +434,37 @@ __device__ inline void store_partial(float* sbase, int nrows, int j, int g, cons
     }
 }
 
-constexpr int kMergeBatch = 8;  // pieces whose loads are in flight together in a merge
+// Pieces whose loads are in flight together in a merge: segments of up to
+// kMergeBatch pieces take one round, longer ones rounds of kMergeBatchLong (a
+// merge kernel lasts as long as its segment with the most pieces, and every
+// round is a dependent memory round trip).
+constexpr int kMergeBatch = 8;
+constexpr int kMergeBatchLong = 16;
 
 // Merge of the pieces [base, base + cnt) of one segment (slots of slot_floats
 // floats from part) for slot row j of nrows, NQ runs of eight dims starting at
 // d[q]: the base-2-LSE-weighted sum of the pieces' normalised outputs
-// (paged_kernel_v21.cuh:325-364), with kMergeBatch pieces' loads in flight per
-// round.  res[q][e] = merged value of dim d[q] + e; 0 when no piece has a
-// visible key.  The split-merge kernels (one run per thread) and the in-kernel
-// merge of the decode kernel (four runs per lane) share this code, so both give
-// the same bits for the same pieces.
-template <int DT, int NQ>
-__device__ inline void merge_runs(const float* part, long long slot_floats, int nrows, int j, const int (&d)[NQ],
-                                  int base, int cnt, float (&res)[NQ][8]) {
+// (paged_kernel_v21.cuh:325-364), with B pieces' loads in flight per round
+// (merge_runs: B = kMergeBatch up to kMergeBatch pieces, else kMergeBatchLong).
+// res[q][e] = merged value of dim d[q] + e; 0 when no piece has a visible key.
+// The result depends on the pieces and on B (the running max is raised once
+// per round).
+template <int DT, int NQ, int B>
+__device__ inline void merge_runs_b(const float* part, long long slot_floats, int nrows, int j, const int (&d)[NQ],
+                                    int base, int cnt, float (&res)[NQ][8]) {
     float m = -DV_INF, wsum = 0.0f;
     float acc[NQ][8];
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
         for (int e = 0; e < 8; ++e) acc[q][e] = 0.0f;
-    for (int k0 = 0; k0 < cnt; k0 += kMergeBatch) {
-        float lse[kMergeBatch];
-        int kx[kMergeBatch];
-        u32x4 h[kMergeBatch][NQ];
-        f32x4 v0[kMergeBatch][NQ], v1[kMergeBatch][NQ];
+    for (int k0 = 0; k0 < cnt; k0 += B) {
+        float lse[B];
+        int kx[B];
+        u32x4 h[B][NQ];
+        f32x4 v0[B][NQ], v1[B][NQ];
 #pragma unroll
-        for (int i = 0; i < kMergeBatch; ++i) {
+        for (int i = 0; i < B; ++i) {
             const bool in = k0 + i < cnt;
             const float* sp = part + (long long)(base + (in ? k0 + i : k0)) * slot_floats;
             lse[i] = in ? sp[nrows * kHeadDim + j] : -DV_INF;
@@ -477,7 +482,7 @@ __device__ inline void merge_runs(const float* part, long long slot_floats, int 
         }
         float bm = m;
 #pragma unroll
-        for (int i = 0; i < kMergeBatch; ++i) bm = fmaxf(bm, lse[i]);
+        for (int i = 0; i < B; ++i) bm = fmaxf(bm, lse[i]);
         if (bm == -DV_INF) continue;
         const float sc = exp2f(m - bm);  // m == -inf -> 0
         wsum *= sc;
@@ -486,7 +491,7 @@ __device__ inline void merge_runs(const float* part, long long slot_floats, int 
 #pragma unroll
             for (int e = 0; e < 8; ++e) acc[q][e] *= sc;
 #pragma unroll
-        for (int i = 0; i < kMergeBatch; ++i) {
+        for (int i = 0; i < B; ++i) {
             const float wgt = exp2f(lse[i] - bm);  // empty piece (-inf) -> 0
             wsum += wgt;
             if constexpr (kHalfPartials<DT>) {
@@ -520,6 +525,15 @@ __device__ inline void merge_runs(const float* part, long long slot_floats, int 
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
         for (int e = 0; e < 8; ++e) res[q][e] = acc[q][e] * inv;
+}
+
+template <int DT, int NQ>
+__device__ inline void merge_runs(const float* part, long long slot_floats, int nrows, int j, const int (&d)[NQ],
+                                  int base, int cnt, float (&res)[NQ][8]) {
+    if (cnt <= kMergeBatch)
+        merge_runs_b<DT, NQ, kMergeBatch>(part, slot_floats, nrows, j, d, base, cnt, res);
+    else
+        merge_runs_b<DT, NQ, kMergeBatchLong>(part, slot_floats, nrows, j, d, base, cnt, res);
 }
 
 // Eight merged values stored to the output (16-bit: one 16-byte store).
