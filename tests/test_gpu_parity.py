@@ -440,14 +440,22 @@ def test_varlen_vs_oracle(dv, gpu, dtype, case):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("R", [32, 64])
-def test_varlen_multiview_query_load_paths_bit_identical(dv, gpu, dtype, R):
+@pytest.mark.parametrize("F,skips", [(3, False), (6, False), (4, True)])
+def test_varlen_multiview_query_load_paths_bit_identical(dv, gpu, dtype, R, F, skips):
     """Varlen rows over several views (configuration 3's shape of call): the
     early query load of the multi-view stream (the row's query runs once, each
     view's half-width cos/sin) against the one-step load forced by cos/sin at a
-    4-byte offset -- equal bit for bit, and equal to the oracle."""
+    4-byte offset -- equal bit for bit, and equal to the oracle.  Six views is
+    more than one stream of views takes; with skips, some tokens' views have
+    location -1 (skipped, their cos/sin never used)."""
     from dvattention_amd import capi
-    d = rand_varlen(3, 8, 8, list(range(9)), 4, 16, [400, 350, 500], R, dtype, seed=40 + R)
-    d["locations"] = torch.from_numpy(np.random.default_rng(5).integers(100, 350, size=(3, 8)).astype(np.int32))
+    lens = [400, 350, 500, 120, 260, 90][:F]
+    d = rand_varlen(F, 8, 8, list(range(9)), 4, 16, lens, R, dtype, seed=40 + R + F)
+    rng = np.random.default_rng(5 + F)
+    loc = rng.integers(60, 350, size=(F, 8)).astype(np.int32)
+    if skips:
+        loc[rng.random(size=(F, 8)) < 0.35] = -1
+    d["locations"] = torch.from_numpy(loc)
     g = to(d, gpu)
     a = torch.empty(8, 64, 128, dtype=dtype, device=gpu)
     capi.varlen_paged_sdpa(a, 0.07, g["locations"], g["queries"], g["cosines"], g["sines"], g["fragment_lengths"],
