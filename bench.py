@@ -521,8 +521,9 @@ def cpu_baseline(device, budget_s: float = 10.0) -> dict:
     median run time gives the rate."""
     from dvattention_amd import workloads as WL
     from oracle import dvattn_oracle as O
-    # every core of the host (BASELINE.md's protocol): os.cpu_count(), which on
-    # the MI355X box equals its scheduler affinity and its cgroup CPU quota
+    # every core of the host (the CPU baseline's protocol: all cores the
+    # process may use): os.cpu_count(), which on the MI355X box equals its
+    # scheduler affinity and its cgroup CPU quota
     cores = os.cpu_count() or 1
     torch.set_num_threads(cores)
     avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else cores
