@@ -691,17 +691,24 @@ __global__ __launch_bounds__(256) void dv_stream(const DecodeParams p) {
 
 // ---- split merge -------------------------------------------------------------------
 
-// Block (segment, KV head, quarter of the head dims) with one wave: thread t
-// handles query head t/4, dims [q*32 + (t%4)*8, +8).  count == 1: already final;
-// count == 0: no visible key -> zeros (paged_kernel_v21.cuh:318); otherwise the
-// base-2-LSE-weighted sum of the pieces' normalised outputs (merge_runs,
-// paged_kernel_v21.cuh:325-364).  The quarters spread a long segment's partials
-// (up to ~40 pieces x 8 KiB per KV head) over four CUs: one CU reads at only
-// ~50-100 GB/s, which set the merge time of segments with many pieces.
+// Block (segment, KV head, quarter of the head dims) with four waves: thread
+// t of a wave handles query head t/4, dims [q*32 + (t%4)*8, +8).  count == 1:
+// already final; count == 0: no visible key -> zeros (paged_kernel_v21.cuh:318);
+// otherwise the base-2-LSE-weighted sum of the pieces' normalised outputs
+// (merge_runs, paged_kernel_v21.cuh:325-364).  The quarters spread a long
+// segment's partials (up to ~40 pieces x 8 KiB per KV head) over four CUs: one
+// CU reads at only ~50-100 GB/s, which set the merge time of segments with
+// many pieces.  Segments of up to kMergeBatchLong pieces are merged by wave 0
+// alone (one round of loads); longer ones by all four waves, wave w taking the
+// w-th quarter of the pieces in one round, and wave 0 combines the four
+// partial sums (their maxima, weight sums and weighted sums) through LDS --
+// a merge kernel lasts as long as its segment with the most pieces.
 constexpr int kMergeQuarters = 4;
+constexpr int kMergeWaves = 4;
 
 template <int DT, int RM>
-__global__ __launch_bounds__(64) void dv_merge(const DecodeParams p) {
+__global__ __launch_bounds__(kMergeWaves * kWave) void dv_merge(const DecodeParams p) {
+    __shared__ float s_part[kMergeWaves - 1][10][kWave];  // waves 1..3: m, wsum, acc[8] per lane
     const int qi = blockIdx.x % kMergeQuarters;
     const int sw = blockIdx.x / kMergeQuarters;
     const int sg = sw / p.hpw;
@@ -709,12 +716,65 @@ __global__ __launch_bounds__(64) void dv_merge(const DecodeParams p) {
     const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
     if (cnt == 1) return;
     const int NHG = p.Hkv / p.hpw;
-    const int n = threadIdx.x >> 2;
+    const int wv = threadIdx.x / kWave, t = threadIdx.x % kWave;
+    const int n = t >> 2;
     const int r = sg / NHG, hg = sg - (sg / NHG) * NHG;
-    const int d[1] = {qi * 32 + (int)(threadIdx.x & 3) * 8};
-    float v[1][8];
-    merge_runs<DT, 1>(p.part, p.slot_floats, p.hpw * kGqa, wi * kGqa + n, d, base, cnt, v);
-    store_run8<DT>(out_row_ptr<DT, RM>(p, p.row_begin + r, (hg * p.hpw + wi) * kGqa + n) + d[0], v[0]);
+    const int d[1] = {qi * 32 + (t & 3) * 8};
+    typename Tr<DT>::raw* o = out_row_ptr<DT, RM>(p, p.row_begin + r, (hg * p.hpw + wi) * kGqa + n) + d[0];
+    if (cnt <= kMergeBatchLong) {  // uniform: the other waves leave before any barrier
+        if (wv != 0) return;
+        float v[1][8];
+        merge_runs<DT, 1>(p.part, p.slot_floats, p.hpw * kGqa, wi * kGqa + n, d, base, cnt, v);
+        store_run8<DT>(o, v[0]);
+        return;
+    }
+    // consecutive quarters of the pieces: with cnt > kMergeBatchLong every
+    // quarter is non-empty (3 * ceil(cnt / 4) < cnt), and one round long while
+    // cnt <= 4 * kMergeBatchLong
+    const int per = (cnt + kMergeWaves - 1) / kMergeWaves;
+    const int b0 = wv * per;
+    const int c0 = cnt - b0 < per ? cnt - b0 : per;
+    float m, wsum, acc[1][8];
+    merge_acc_b<DT, 1, kMergeBatchLong>(p.part, p.slot_floats, p.hpw * kGqa, wi * kGqa + n, d, base + b0, c0, m, wsum,
+                                        acc);
+    if (wv > 0) {
+        s_part[wv - 1][0][t] = m;
+        s_part[wv - 1][1][t] = wsum;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s_part[wv - 1][2 + e][t] = acc[0][e];
+    }
+    __syncthreads();
+    if (wv != 0) return;
+    float mw[kMergeWaves], ww[kMergeWaves], M = m;
+    mw[0] = m;
+    ww[0] = wsum;
+#pragma unroll
+    for (int w = 1; w < kMergeWaves; ++w) {
+        mw[w] = s_part[w - 1][0][t];
+        ww[w] = s_part[w - 1][1][t];
+        M = fmaxf(M, mw[w]);
+    }
+    float v[8];
+    if (M == -DV_INF) {  // no piece has a visible key
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = 0.0f;
+    } else {
+        float sc[kMergeWaves], tw = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kMergeWaves; ++w) {
+            sc[w] = exp2f(mw[w] - M);  // a quarter without visible keys (-inf) -> 0
+            tw += ww[w] * sc[w];
+        }
+        const float inv = tw > 0.0f ? 1.0f / tw : 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float a = acc[0][e] * sc[0];
+#pragma unroll
+            for (int w = 1; w < kMergeWaves; ++w) a += s_part[w - 1][2 + e][t] * sc[w];
+            v[e] = a * inv;
+        }
+    }
+    store_run8<DT>(o, v);
 }
 
 // ---- host side --------------------------------------------------------------------
@@ -788,7 +848,8 @@ hipError_t launch_one(DecodeParams p, int device, long long max_wg, long long ca
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return note_site(e, "launch decode");
     const int nseg = p.nrows * (p.Hkv / p.hpw);
-    hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg * p.hpw * kMergeQuarters), dim3(kWave), 0, stream, p);
+    hipLaunchKernelGGL((dv_merge<DT, RM>), dim3(nseg * p.hpw * kMergeQuarters), dim3(kMergeWaves * kWave), 0,
+                       stream, p);
     e = hipGetLastError();
     if (e != hipSuccess) return note_site(e, "launch dv_merge");
     return hipSuccess;

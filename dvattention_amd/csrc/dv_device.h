@@ -449,11 +449,13 @@ constexpr int kMergeBatchLong = 16;
 // res[q][e] = merged value of dim d[q] + e; 0 when no piece has a visible key.
 // The result depends on the pieces and on B (the running max is raised once
 // per round).
+// merge_acc_b: the accumulation -- the running base-2 max m_out, the weight
+// sum wsum_out and the weighted sum acc over the pieces (-inf, 0 and zeros for
+// none); merge_runs_b normalises it.
 template <int DT, int NQ, int B>
-__device__ inline void merge_runs_b(const float* part, long long slot_floats, int nrows, int j, const int (&d)[NQ],
-                                    int base, int cnt, float (&res)[NQ][8]) {
+__device__ inline void merge_acc_b(const float* part, long long slot_floats, int nrows, int j, const int (&d)[NQ],
+                                   int base, int cnt, float& m_out, float& wsum_out, float (&acc)[NQ][8]) {
     float m = -DV_INF, wsum = 0.0f;
-    float acc[NQ][8];
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
@@ -520,6 +522,15 @@ __device__ inline void merge_runs_b(const float* part, long long slot_floats, in
         }
         m = bm;
     }
+    m_out = m;
+    wsum_out = wsum;
+}
+
+template <int DT, int NQ, int B>
+__device__ inline void merge_runs_b(const float* part, long long slot_floats, int nrows, int j, const int (&d)[NQ],
+                                    int base, int cnt, float (&res)[NQ][8]) {
+    float m, wsum, acc[NQ][8];
+    merge_acc_b<DT, NQ, B>(part, slot_floats, nrows, j, d, base, cnt, m, wsum, acc);
     const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
