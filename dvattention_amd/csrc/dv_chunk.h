@@ -208,11 +208,13 @@ __global__ __launch_bounds__(256) void dv_merge_chunk(const DecodeParams p) {
     using raw = typename Tr<DT>::raw;
     const int sg = blockIdx.x / kTokBlk;
     const int tb = blockIdx.x - sg * kTokBlk;
-    const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
-    if (cnt == 1) return;
     const int NHG = p.Hkv;
     const int r = sg / NHG, hkv = sg - (sg / NHG) * NHG;
+    // the group (a table load for varlen rows) and the directory entry are
+    // loaded together: one round trip instead of two
     const Grp gr = group_of<RM>(p, p.row_begin + r);
+    const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
+    if (cnt == 1) return;
     if (tb >= gr.ntok) return;
     const int tid = threadIdx.x;
     const int n = tid >> 4;
