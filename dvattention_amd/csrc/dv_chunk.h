@@ -208,13 +208,11 @@ __global__ __launch_bounds__(256) void dv_merge_chunk(const DecodeParams p) {
     using raw = typename Tr<DT>::raw;
     const int sg = blockIdx.x / kTokBlk;
     const int tb = blockIdx.x - sg * kTokBlk;
-    const int NHG = p.Hkv;
-    const int r = sg / NHG, hkv = sg - (sg / NHG) * NHG;
-    // the group (a table load for varlen rows) and the directory entry are
-    // loaded together: one round trip instead of two
-    const Grp gr = group_of<RM>(p, p.row_begin + r);
     const int base = p.dir[2 * sg], cnt = p.dir[2 * sg + 1];
     if (cnt == 1) return;
+    const int NHG = p.Hkv;
+    const int r = sg / NHG, hkv = sg - (sg / NHG) * NHG;
+    const Grp gr = group_of<RM>(p, p.row_begin + r);
     if (tb >= gr.ntok) return;
     const int tid = threadIdx.x;
     const int n = tid >> 4;
@@ -222,7 +220,10 @@ __global__ __launch_bounds__(256) void dv_merge_chunk(const DecodeParams p) {
     const int h = hkv * kGqa + n;
     raw* o = reinterpret_cast<raw*>(p.out) + out_row<RM>(p, gr, tb, h) + d[0];
     float v[1][8];
-    merge_runs<DT, 1>(p.part, p.slot_floats, kTokBlk * kGqa, tb * kGqa + n, d, base, cnt, v);
+    // rounds of 8 pieces: a chunk segment rarely has more (configuration 5: two),
+    // and the 16-piece round's registers would cost this 256-thread kernel a
+    // wave per SIMD of occupancy
+    merge_runs_b<DT, 1, kMergeBatch>(p.part, p.slot_floats, kTokBlk * kGqa, tb * kGqa + n, d, base, cnt, v);
     store_run8<DT>(o, v[0]);
 }
 
